@@ -1,0 +1,148 @@
+/*
+ * minivllm_hip.h -- C ABI of libminivllm_hip.so, the MI355X (gfx950) paged-KV
+ * decode hot path of the minivllm runtime.
+ *
+ * Plain C: raw device pointers, element strides, sizes and enums. No torch
+ * types. Every compute entry point is asynchronous on the given HIP stream
+ * (NULL = the legacy default stream) and returns an int status:
+ *
+ *   MGI_OK (0)           launched (or nothing to do)
+ *   MGI_EINVAL (-1)      an argument violates the contract (shape, stride,
+ *                        alignment, range, null pointer)
+ *   MGI_EUNSUPPORTED(-2) a valid request this library does not implement
+ *   MGI_ELAUNCH (-3)     the HIP runtime refused the launch
+ *   MGI_EWORKSPACE (-4)  workspace missing or smaller than required
+ *
+ * On a non-zero status, mgi_last_error() returns a thread-local message.
+ * No entry point synchronises the stream or reads device data on the host:
+ * device-data invariants (context lengths >= 1, valid block-table entries for
+ * every block a context touches) are the caller's, exactly as for the
+ * reference backends. The kernels never read or write outside the buffers
+ * described by the sizes given: out-of-range slots, block ids and context
+ * lengths are skipped or clamped on the device.
+ *
+ * Layouts (element strides, row-major by default):
+ *   KV pool      [L, N, S, H, D]   (KVBlockPool.k / .v)
+ *   q, out       [B, H, D]         (any strides)
+ *   k_new, v_new [T, H, D]         (any strides; T rows written)
+ *   block_tables [B, M]            (int32 or int64; -1 padding in the tail)
+ *   context_lens [B]               (int32 or int64; includes the new token)
+ *   slot_mapping [T]               (int32 or int64; slot = block*S + offset;
+ *                                   a negative slot means "skip this row")
+ */
+#ifndef MINIVLLM_HIP_H
+#define MINIVLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum mgi_status {
+  MGI_OK = 0,
+  MGI_EINVAL = -1,
+  MGI_EUNSUPPORTED = -2,
+  MGI_ELAUNCH = -3,
+  MGI_EWORKSPACE = -4
+};
+
+/* Element types of q / out / KV pool / new K,V. */
+enum mgi_dtype { MGI_F32 = 0, MGI_BF16 = 1, MGI_F16 = 2 };
+
+/* Element types of block tables, context lengths and slot mappings. */
+enum mgi_itype { MGI_I32 = 0, MGI_I64 = 1 };
+
+/* Thread-local description of the last failing call ("" if none). */
+const char* mgi_last_error(void);
+
+/* ABI version of this library (major*100 + minor). */
+int mgi_abi_version(void);
+
+/*
+ * KV append / scatter.
+ * Replaces the inline decode KV write of
+ * KVCacheCausalSelfAttention.forward_decode_batch
+ * (minivllm/attention.py:370-392: physical_blocks = slots // S,
+ * block_offsets = slots % S, pool.k[layer, blk, off] = k, same for v) and the
+ * per-token prefill write loop that calls KVBlockPool.write_layer
+ * (minivllm/attention.py:190-208, minivllm/kv_block_pool.py:91-109).
+ *
+ * For every row t < T with s = slot_mapping[t] and 0 <= s < N*S:
+ *   k_pool[layer_idx, s / S, s % S, :, :] = k_new[t, :, :]
+ *   v_pool[layer_idx, s / S, s % S, :, :] = v_new[t, :, :]
+ * Rows with s < 0 (padding) or s >= N*S are skipped; nothing else in the pool
+ * is touched. With new_dtype == pool_dtype the copy is bit-exact; otherwise
+ * the value is converted with round-to-nearest-even (f32 -> bf16/f16) or
+ * exactly (bf16/f16 -> f32). Other conversions return MGI_EUNSUPPORTED.
+ * If two rows name the same slot, which one lands is unspecified (as for
+ * torch index_put_ without accumulate).
+ */
+int mgi_kv_append(void* k_pool, void* v_pool,
+                  const int64_t* k_pool_strides, /* [5] */
+                  const int64_t* v_pool_strides, /* [5] */
+                  int pool_dtype,
+                  const void* k_new, const void* v_new,
+                  const int64_t* k_new_strides, /* [3] */
+                  const int64_t* v_new_strides, /* [3] */
+                  int new_dtype,
+                  const void* slot_mapping, int64_t slot_stride, int slot_itype,
+                  int64_t T, int64_t H, int64_t D,
+                  int64_t S, int64_t N, int64_t L, int64_t layer_idx,
+                  void* stream);
+
+/*
+ * Paged decode attention (one query token per sequence).
+ * Replaces paged_attention_batch_online_v1
+ * (minivllm/paged_attention_batch.py:121-278) and
+ * paged_attention_batch_triton_v0 / _paged_decode_f32
+ * (minivllm/triton_paged_decode.py:29-155).
+ *
+ * For b < B, h < H, with c = context_lens[b] (clamped to [0, M*S]):
+ *   out[b,h,:] = sum_t softmax_t(scale * q[b,h,:] . K[t,h,:]) * V[t,h,:]
+ * over the c logical tokens t, where token t lives in physical block
+ * block_tables[b, t / S] at offset t % S of layer layer_idx. Only those
+ * tokens are read: table entries past ceil(c/S) are never loaded and slots
+ * past c are never dereferenced. A table entry outside [0, N) inside the
+ * context is treated as a fully masked block. c == 0 gives out = 0 (the
+ * online_v1 result for a row with no active block).
+ * q, out and the pool share one dtype; arithmetic is fp32.
+ *
+ * split_tokens: tokens per context partition for the split-context pass
+ * (0 = choose automatically; otherwise rounded to a multiple of S). Contexts
+ * longer than one partition are processed as independent partitions whose
+ * (max, sum, unnormalised output) partials are merged by a second pass.
+ * workspace must hold mgi_paged_decode_workspace_bytes(...) bytes for the
+ * same (B, H, D, S, M, split_tokens); it may be NULL when that is 0.
+ */
+int mgi_paged_decode(void* out, const int64_t* out_strides, /* [3] */
+                     const void* q, const int64_t* q_strides, /* [3] */
+                     const void* k_pool, const void* v_pool,
+                     const int64_t* k_pool_strides, /* [5] */
+                     const int64_t* v_pool_strides, /* [5] */
+                     int dtype,
+                     const void* block_tables, const int64_t* bt_strides, /* [2] */
+                     int bt_itype,
+                     const void* context_lens, int64_t cl_stride, int cl_itype,
+                     int64_t B, int64_t H, int64_t D, int64_t S, int64_t N,
+                     int64_t M, int64_t L, int64_t layer_idx,
+                     float scale, int64_t split_tokens,
+                     void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Workspace bytes mgi_paged_decode needs for these sizes (0 if none). */
+size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D,
+                                        int64_t S, int64_t M,
+                                        int64_t split_tokens);
+
+/* The partition size (tokens) mgi_paged_decode uses for these sizes. */
+int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D,
+                                      int64_t S, int64_t M,
+                                      int64_t split_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINIVLLM_HIP_H */

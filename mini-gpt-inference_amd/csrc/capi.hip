@@ -1,0 +1,286 @@
+// capi.hip -- extern "C" entry points of libminivllm_hip.so (declared in
+// include/minivllm_hip.h): argument validation, path selection, workspace
+// layout and launch. Validation mirrors the host checks of
+// paged_attention_batch_triton_v0 (minivllm/triton_paged_decode.py:109-144);
+// nothing here reads device memory or synchronises the stream.
+#include <algorithm>
+#include <cmath>
+#include <string>
+
+#include "mgi_internal.h"
+#include "minivllm_hip.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+bool valid_dtype(int d) { return d == MGI_F32 || d == MGI_BF16 || d == MGI_F16; }
+bool valid_itype(int t) { return t == MGI_I32 || t == MGI_I64; }
+int64_t dtype_bytes(int d) { return d == MGI_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool mult16(int64_t elems, int64_t eb) { return (elems * eb) % 16 == 0; }
+
+bool nonneg(const int64_t* s, int n) {
+  for (int i = 0; i < n; ++i)
+    if (s[i] < 0) return false;
+  return true;
+}
+
+constexpr int64_t kMaxGridYZ = 65535;
+constexpr int64_t kWorkspaceAlign = 256;
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Partition size in tokens: a multiple of S, one partition when the whole
+// table fits, and at most kMaxGridYZ partitions per sequence.
+int64_t split_tokens_for(int64_t S, int64_t M, int64_t requested) {
+  const int64_t max_ctx = M * S;
+  int64_t P = requested;
+  if (P <= 0) {
+    P = 256;
+    while (P * 1024 < max_ctx) P *= 2;  // keep <= 1024 partitions per sequence
+  }
+  P = round_up(P, S);
+  while ((max_ctx + P - 1) / P > kMaxGridYZ) P = round_up(P * 2, S);
+  if (P >= max_ctx) P = max_ctx;
+  return P;
+}
+
+struct WorkspaceLayout {
+  size_t acc_bytes, ml_offset, total;
+  int64_t max_parts;
+};
+
+WorkspaceLayout workspace_layout(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
+                                 int64_t P) {
+  WorkspaceLayout w{};
+  w.max_parts = (M * S + P - 1) / P;
+  if (w.max_parts <= 1) return w;
+  const int64_t n = B * H * w.max_parts;
+  w.acc_bytes = (size_t)(n * D * 4);
+  w.ml_offset = (size_t)round_up((int64_t)w.acc_bytes, kWorkspaceAlign);
+  w.total = w.ml_offset + (size_t)(n * 8);
+  return w;
+}
+
+int next_pow2_at_least4(int64_t x) {
+  int p = 4;
+  while (p < x) p *= 2;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mgi_last_error(void) { return g_err.c_str(); }
+
+int mgi_abi_version(void) { return 100; }
+
+int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
+                                      int64_t split_tokens) {
+  (void)B;
+  (void)H;
+  (void)D;
+  if (S <= 0 || M <= 0) return 0;
+  return split_tokens_for(S, M, split_tokens);
+}
+
+size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
+                                        int64_t split_tokens) {
+  if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || M <= 0) return 0;
+  const int64_t P = split_tokens_for(S, M, split_tokens);
+  return workspace_layout(B, H, D, S, M, P).total;
+}
+
+int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
+                     const int64_t* q_strides, const void* k_pool, const void* v_pool,
+                     const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
+                     const void* block_tables, const int64_t* bt_strides, int bt_itype,
+                     const void* context_lens, int64_t cl_stride, int cl_itype, int64_t B,
+                     int64_t H, int64_t D, int64_t S, int64_t N, int64_t M, int64_t L,
+                     int64_t layer_idx, float scale, int64_t split_tokens, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  using namespace mgi;
+  g_err.clear();
+  if (!out || !q || !k_pool || !v_pool || !block_tables || !context_lens)
+    return fail(MGI_EINVAL, "null tensor pointer");
+  if (!out_strides || !q_strides || !k_pool_strides || !v_pool_strides || !bt_strides)
+    return fail(MGI_EINVAL, "null stride array");
+  if (B <= 0 || H <= 0 || D <= 0) return fail(MGI_EINVAL, "q dimensions must be nonzero");
+  if (S <= 0 || N <= 0 || L <= 0) return fail(MGI_EINVAL, "pool dimensions must be nonzero");
+  if (M < 1) return fail(MGI_EINVAL, "block_tables need at least one block column");
+  if (layer_idx < 0 || layer_idx >= L) return fail(MGI_EINVAL, "layer_idx outside KV pool");
+  if (!valid_dtype(dtype)) return fail(MGI_EINVAL, "unknown dtype code");
+  if (!valid_itype(bt_itype) || !valid_itype(cl_itype))
+    return fail(MGI_EINVAL, "index arrays must be int32 or int64");
+  if (!std::isfinite(scale)) return fail(MGI_EINVAL, "scale must be finite");
+  if (!nonneg(out_strides, 3) || !nonneg(q_strides, 3) || !nonneg(k_pool_strides, 5) ||
+      !nonneg(v_pool_strides, 5) || !nonneg(bt_strides, 2) || cl_stride < 0)
+    return fail(MGI_EINVAL, "strides must be non-negative");
+  if (B > kMaxGridYZ) return fail(MGI_EUNSUPPORTED, "batch larger than 65535");
+  if (M * S >= (int64_t(1) << 31)) return fail(MGI_EUNSUPPORTED, "M*S must be < 2^31");
+  if (D > 512) return fail(MGI_EUNSUPPORTED, "head_dim larger than 512");
+
+  const int64_t eb = dtype_bytes(dtype);
+  const char* kbase = static_cast<const char*>(k_pool) + layer_idx * k_pool_strides[0] * eb;
+  const char* vbase = static_cast<const char*>(v_pool) + layer_idx * v_pool_strides[0] * eb;
+
+  const int64_t P = split_tokens_for(S, M, split_tokens);
+  const WorkspaceLayout ws = workspace_layout(B, H, D, S, M, P);
+
+  // Path selection: the fast kernel needs unit d-stride, 16-byte aligned head
+  // rows, head_dim a multiple of 8 up to 256 and S a multiple of its step.
+  DecodePlan plan{};
+  plan.path = DecodePath::kGeneric;
+  const int64_t row_span = ((H - 1) * std::max(k_pool_strides[3], v_pool_strides[3]) + D) * eb;
+  if ((dtype == MGI_BF16 || dtype == MGI_F32) && D % 8 == 0 && D <= 256 &&
+      k_pool_strides[4] == 1 && v_pool_strides[4] == 1 && aligned16(kbase) &&
+      aligned16(vbase) && mult16(k_pool_strides[1], eb) && mult16(k_pool_strides[2], eb) &&
+      mult16(k_pool_strides[3], eb) && mult16(v_pool_strides[1], eb) &&
+      mult16(v_pool_strides[2], eb) && mult16(v_pool_strides[3], eb) &&
+      row_span < (int64_t(1) << 31) &&
+      std::max(k_pool_strides[2], v_pool_strides[2]) * eb * S < (int64_t(1) << 31)) {
+    int tok = 0;
+    if (dtype == MGI_BF16 && S % 16 == 0) tok = 16;
+    else if (S % 8 == 0) tok = 8;
+    if (tok) {
+      plan.path = DecodePath::kFast;
+      plan.tokens_per_step = tok;
+      plan.lanes_per_head = next_pow2_at_least4(D / 8);
+      plan.full_lanes = (D == 8 * plan.lanes_per_head) && (H % (64 / plan.lanes_per_head) == 0);
+    }
+  }
+
+  DecodeArgs a{};
+  a.out = out;
+  a.o_sb = out_strides[0];
+  a.o_sh = out_strides[1];
+  a.o_sd = out_strides[2];
+  a.q = q;
+  a.q_sb = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.q_sd = q_strides[2];
+  a.k = kbase;
+  a.v = vbase;
+  a.k_sn = k_pool_strides[1];
+  a.k_ss = k_pool_strides[2];
+  a.k_sh = k_pool_strides[3];
+  a.k_sd = k_pool_strides[4];
+  a.v_sn = v_pool_strides[1];
+  a.v_ss = v_pool_strides[2];
+  a.v_sh = v_pool_strides[3];
+  a.v_sd = v_pool_strides[4];
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sm = bt_strides[1];
+  a.cl = context_lens;
+  a.cl_s = cl_stride;
+  a.bt_i64 = bt_itype == MGI_I64;
+  a.cl_i64 = cl_itype == MGI_I64;
+  a.B = (int)B;
+  a.H = (int)H;
+  a.D = (int)D;
+  a.S = (int)S;
+  a.M = (int)M;
+  a.N = N;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.part_tokens = (int)P;
+  a.max_parts = plan.path == DecodePath::kFast ? (int)ws.max_parts : 1;
+  if (a.max_parts > 1) {
+    if (!workspace) return fail(MGI_EWORKSPACE, "workspace required for split-context pass");
+    if (workspace_bytes < ws.total)
+      return fail(MGI_EWORKSPACE, "workspace smaller than mgi_paged_decode_workspace_bytes()");
+    if (!aligned16(workspace)) return fail(MGI_EINVAL, "workspace must be 16-byte aligned");
+    a.ws_acc = static_cast<float*>(workspace);
+    a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + ws.ml_offset);
+  } else {
+    a.part_tokens = (int)(M * S);  // one partition covers every context
+  }
+
+  const hipError_t e = launch_paged_decode(a, dtype, plan, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MGI_ELAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
+  return MGI_OK;
+}
+
+int mgi_kv_append(void* k_pool, void* v_pool, const int64_t* k_pool_strides,
+                  const int64_t* v_pool_strides, int pool_dtype, const void* k_new,
+                  const void* v_new, const int64_t* k_new_strides, const int64_t* v_new_strides,
+                  int new_dtype, const void* slot_mapping, int64_t slot_stride, int slot_itype,
+                  int64_t T, int64_t H, int64_t D, int64_t S, int64_t N, int64_t L,
+                  int64_t layer_idx, void* stream) {
+  using namespace mgi;
+  g_err.clear();
+  if (T < 0) return fail(MGI_EINVAL, "row count must be non-negative");
+  if (T == 0) return MGI_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping)
+    return fail(MGI_EINVAL, "null tensor pointer");
+  if (!k_pool_strides || !v_pool_strides || !k_new_strides || !v_new_strides)
+    return fail(MGI_EINVAL, "null stride array");
+  if (H <= 0 || D <= 0 || S <= 0 || N <= 0 || L <= 0)
+    return fail(MGI_EINVAL, "pool dimensions must be nonzero");
+  if (layer_idx < 0 || layer_idx >= L) return fail(MGI_EINVAL, "layer_idx outside KV pool");
+  if (!valid_dtype(pool_dtype) || !valid_dtype(new_dtype)) return fail(MGI_EINVAL, "unknown dtype code");
+  if (!valid_itype(slot_itype)) return fail(MGI_EINVAL, "slot_mapping must be int32 or int64");
+  if (!nonneg(k_pool_strides, 5) || !nonneg(v_pool_strides, 5) || !nonneg(k_new_strides, 3) ||
+      !nonneg(v_new_strides, 3) || slot_stride < 0)
+    return fail(MGI_EINVAL, "strides must be non-negative");
+  if (T > (int64_t(1) << 31) - 1) return fail(MGI_EUNSUPPORTED, "too many rows");
+  if (pool_dtype != new_dtype && pool_dtype != MGI_F32 && new_dtype != MGI_F32)
+    return fail(MGI_EUNSUPPORTED, "only same-dtype copies and conversions to/from f32");
+
+  const int64_t peb = dtype_bytes(pool_dtype), neb = dtype_bytes(new_dtype);
+  char* kbase = static_cast<char*>(k_pool) + layer_idx * k_pool_strides[0] * peb;
+  char* vbase = static_cast<char*>(v_pool) + layer_idx * v_pool_strides[0] * peb;
+
+  AppendArgs a{};
+  a.kp = kbase;
+  a.vp = vbase;
+  a.k_sn = k_pool_strides[1];
+  a.k_ss = k_pool_strides[2];
+  a.k_sh = k_pool_strides[3];
+  a.k_sd = k_pool_strides[4];
+  a.v_sn = v_pool_strides[1];
+  a.v_ss = v_pool_strides[2];
+  a.v_sh = v_pool_strides[3];
+  a.v_sd = v_pool_strides[4];
+  a.kn = k_new;
+  a.vn = v_new;
+  a.kn_st = k_new_strides[0];
+  a.kn_sh = k_new_strides[1];
+  a.kn_sd = k_new_strides[2];
+  a.vn_st = v_new_strides[0];
+  a.vn_sh = v_new_strides[1];
+  a.vn_sd = v_new_strides[2];
+  a.slots = slot_mapping;
+  a.sl_s = slot_stride;
+  a.sl_i64 = slot_itype == MGI_I64;
+  a.T = (int)T;
+  a.H = (int)H;
+  a.D = (int)D;
+  a.S = (int)S;
+  a.N = N;
+
+  const bool rows_contig = k_pool_strides[4] == 1 && k_pool_strides[3] == D &&
+                           v_pool_strides[4] == 1 && v_pool_strides[3] == D &&
+                           k_new_strides[2] == 1 && k_new_strides[1] == D &&
+                           v_new_strides[2] == 1 && v_new_strides[1] == D;
+  const bool vector_path = pool_dtype == new_dtype && rows_contig && mult16(H * D, peb) &&
+                           aligned16(kbase) && aligned16(vbase) && aligned16(k_new) &&
+                           aligned16(v_new) && mult16(k_pool_strides[1], peb) &&
+                           mult16(k_pool_strides[2], peb) && mult16(v_pool_strides[1], peb) &&
+                           mult16(v_pool_strides[2], peb) && mult16(k_new_strides[0], neb) &&
+                           mult16(v_new_strides[0], neb);
+
+  const hipError_t e =
+      launch_kv_append(a, pool_dtype, new_dtype, vector_path, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MGI_ELAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
+  return MGI_OK;
+}
+
+}  // extern "C"

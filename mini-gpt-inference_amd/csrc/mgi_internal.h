@@ -1,0 +1,72 @@
+// mgi_internal.h -- argument blocks passed by value to the kernels, and the
+// host-side launchers the C ABI (capi.hip) dispatches to.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mgi {
+
+// Paged decode attention. Pool pointers already point at layer layer_idx.
+// All strides are in elements.
+struct DecodeArgs {
+  void* out;
+  int64_t o_sb, o_sh, o_sd;
+  const void* q;
+  int64_t q_sb, q_sh, q_sd;
+  const void* k;
+  const void* v;
+  int64_t k_sn, k_ss, k_sh, k_sd;
+  int64_t v_sn, v_ss, v_sh, v_sd;
+  const void* bt;
+  int64_t bt_sb, bt_sm;
+  const void* cl;
+  int64_t cl_s;
+  int bt_i64, cl_i64;
+  int B, H, D, S, M;
+  int64_t N;
+  float scale_log2;   // softmax scale * log2(e): scores live in the log2 domain
+  int part_tokens;    // tokens per context partition (multiple of S)
+  int max_parts;      // partitions per sequence covered by the grid
+  float* ws_acc;      // [B, H, max_parts, D] unnormalised partial outputs
+  float2* ws_ml;      // [B, H, max_parts]    partial (max, sum), log2 domain
+};
+
+// KV append / scatter. Pool pointers already point at layer layer_idx.
+struct AppendArgs {
+  void* kp;
+  void* vp;
+  int64_t k_sn, k_ss, k_sh, k_sd;
+  int64_t v_sn, v_ss, v_sh, v_sd;
+  const void* kn;
+  const void* vn;
+  int64_t kn_st, kn_sh, kn_sd;
+  int64_t vn_st, vn_sh, vn_sd;
+  const void* slots;
+  int64_t sl_s;
+  int sl_i64;
+  int T, H, D, S;
+  int64_t N;
+};
+
+enum class DecodePath { kFast, kGeneric };
+
+// Paged decode: how a call will run (decided from dtype, shapes, strides and
+// pointer alignment) and the launchers.
+struct DecodePlan {
+  DecodePath path;
+  int lanes_per_head;   // fast path: lanes that share one head row
+  int tokens_per_step;  // fast path: tokens loaded per inner step
+  bool full_lanes;      // fast path: every lane maps to a valid (head, d)
+};
+
+hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan& plan,
+                               hipStream_t stream);
+
+// KV append launchers. `vector_path` copies 16-byte chunks (same dtype,
+// contiguous aligned rows); otherwise an element loop converts dtypes.
+hipError_t launch_kv_append(const AppendArgs& a, int pool_dtype, int new_dtype,
+                            bool vector_path, hipStream_t stream);
+
+}  // namespace mgi

@@ -1,0 +1,430 @@
+// paged_decode.hip -- paged decode attention for gfx950 (CDNA4, wave64).
+//
+// Semantics follow paged_attention_batch_online_v1
+// (minivllm/paged_attention_batch.py:121-278) and the Triton v0 kernel
+// (minivllm/triton_paged_decode.py:29-99): for each (sequence b, head h)
+//   out = softmax(scale * q . K^T) V  over the ctx_b valid tokens reached
+// through block_tables[b, 0 : ceil(ctx_b / S)]. Table entries past the
+// context and pool slots past the context are never dereferenced.
+//
+// Fast path (paged_decode_fast): one wavefront owns HPW = 64/LPH heads of one
+// sequence and one context partition. LPH lanes share a head row, each lane
+// owning 8 elements of head_dim, so one 16-byte load instruction of the wave
+// reads a contiguous run of HPW head rows of one token (1 KiB for bf16,
+// D=128). Per step the wave issues TOK tokens of K and V loads up front
+// (32 KiB in flight per wave for bf16, TOK=16), then forms the TOK scores with
+// packed bf16 dot products and a DPP all-reduce inside each 16-lane row, and
+// folds the step into an fp32 online softmax kept in the log2 domain.
+// Decode attention is HBM-bound (~1 flop/byte), so there is no MFMA and no
+// LDS staging: every lane loads exactly the bytes it consumes.
+//
+// Contexts longer than one partition write (max, sum, unnormalised output)
+// partials that paged_decode_merge combines:
+//   M = max_p m_p,  L = sum_p l_p 2^(m_p - M),  O = sum_p O_p 2^(m_p - M) / L.
+//
+// Generic path (paged_decode_generic): any strides, head_dim up to 512, any
+// block size, f32/bf16/f16; one wavefront per (b, h), one token at a time.
+#include "mgi_common.h"
+#include "mgi_internal.h"
+#include "minivllm_hip.h"
+
+namespace mgi {
+
+// ------------------------------------------------------------ lane layout
+// A lane owns 8 elements of one head row.
+//   2-byte types: d = 8*sub + i                       (one 16-byte load)
+//   f32:          d = 4*sub + i            (i < 4)    (two 16-byte loads, each
+//                 d = D/2 + 4*sub + i - 4  (i >= 4)    contiguous across lanes)
+template <typename T> struct Layout;
+template <> struct Layout<bf16_t> {
+  static constexpr int kLoads = 1;
+  __device__ static int load_off(int sub, int /*D*/, int /*j*/) { return 8 * sub; }
+  __device__ static int elem(int sub, int /*D*/, int i) { return 8 * sub + i; }
+};
+template <> struct Layout<float> {
+  static constexpr int kLoads = 2;
+  __device__ static int load_off(int sub, int D, int j) { return j * (D >> 1) + 4 * sub; }
+  __device__ static int elem(int sub, int D, int i) { return (i >> 2) * (D >> 1) + 4 * sub + (i & 3); }
+};
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Element i (0..7) of a lane's raw fragment as f32.
+template <typename T>
+__device__ __forceinline__ float frag_elem(const uint4 (&r)[Layout<T>::kLoads], int i);
+template <>
+__device__ __forceinline__ float frag_elem<bf16_t>(const uint4 (&r)[1], int i) {
+  const uint32_t w = (i >> 1) == 0 ? r[0].x : (i >> 1) == 1 ? r[0].y : (i >> 1) == 2 ? r[0].z : r[0].w;
+  return (i & 1) ? bf16_hi(w) : bf16_lo(w);
+}
+template <>
+__device__ __forceinline__ float frag_elem<float>(const uint4 (&r)[2], int i) {
+  const uint4& x = r[i >> 2];
+  const uint32_t w = (i & 3) == 0 ? x.x : (i & 3) == 1 ? x.y : (i & 3) == 2 ? x.z : x.w;
+  return __uint_as_float(w);
+}
+
+// Query fragment: packed bf16 pairs (exact) for bf16, f32 values for f32.
+template <typename T> struct QFrag;
+template <> struct QFrag<bf16_t> {
+  uint32_t w[4];
+  __device__ __forceinline__ float dot(const uint4 (&k)[1]) const {
+    float d = 0.f;
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[0]),
+                                        __builtin_bit_cast(bf16x2, k[0].x), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[1]),
+                                        __builtin_bit_cast(bf16x2, k[0].y), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[2]),
+                                        __builtin_bit_cast(bf16x2, k[0].z), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[3]),
+                                        __builtin_bit_cast(bf16x2, k[0].w), d, false);
+    return d;
+  }
+  __device__ __forceinline__ void load(const bf16_t* row, int64_t sd, int sub, int D) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(row);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = p[(int64_t)Layout<bf16_t>::elem(sub, D, 2 * j) * sd];
+      const uint32_t hi = p[(int64_t)Layout<bf16_t>::elem(sub, D, 2 * j + 1) * sd];
+      w[j] = lo | (hi << 16);
+    }
+  }
+  __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = 0u; }
+};
+template <> struct QFrag<float> {
+  float f[8];
+  __device__ __forceinline__ float dot(const uint4 (&k)[2]) const {
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d = fmaf(f[i], frag_elem<float>(k, i), d);
+    return d;
+  }
+  __device__ __forceinline__ void load(const float* row, int64_t sd, int sub, int D) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = row[(int64_t)Layout<float>::elem(sub, D, i) * sd];
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = 0.f;
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int b) {
+  const int64_t c = load_index(a.cl, a.cl_i64, (int64_t)b * a.cl_s);
+  const int64_t max_ctx = (int64_t)a.M * a.S;
+  return (int)(c < 0 ? 0 : (c > max_ctx ? max_ctx : c));
+}
+
+// Stores a lane's 8 output elements (acc * inv) into out[b, h, :].
+template <typename T>
+__device__ __forceinline__ void store_out(const DecodeArgs& a, int b, int h, int sub,
+                                          const float (&acc)[8], float inv) {
+  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    Elem<T>::store(orow + (int64_t)Layout<T>::elem(sub, a.D, i) * a.o_sd, acc[i] * inv);
+}
+
+// ------------------------------------------------------------- fast kernel
+template <typename T, int LPH, int TOK, bool FULL>
+__global__ void __launch_bounds__(64)
+paged_decode_fast(const DecodeArgs a) {
+  constexpr int HPW = 64 / LPH;
+  constexpr int NL = Layout<T>::kLoads;
+  constexpr int EB = (int)sizeof(T);
+  const int lane = (int)threadIdx.x;
+  const int sub = lane % LPH;
+  const int row = lane / LPH;
+  const int b = (int)blockIdx.z;
+  const int part = (int)blockIdx.y;
+  const int h = (int)blockIdx.x * HPW + row;
+  const int D = a.D;
+  const bool lane_ok = FULL || (h < a.H && sub * 8 < D);
+
+  const int ctx = clamp_ctx<T>(a, b);
+  const int P = a.part_tokens;
+  const int nparts = (ctx + P - 1) / P;
+  if (part >= (nparts > 0 ? nparts : 1)) return;  // uniform over the wave
+
+  QFrag<T> q;
+  q.zero();
+  if (lane_ok)
+    q.load(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh,
+           a.q_sd, sub, D);
+
+  // Byte offsets of this lane's loads inside one token row of the pool.
+  uint32_t koff[NL], voff[NL];
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    koff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.k_sh + Layout<T>::load_off(sub, D, j)) * EB) : 0u;
+    voff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.v_sh + Layout<T>::load_off(sub, D, j)) * EB) : 0u;
+  }
+
+  float m = -INFINITY, l = 0.f;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+
+  const int t_begin = part * P;
+  const int t_end = min(ctx, t_begin + P);
+  const char* kl = reinterpret_cast<const char*>(a.k);
+  const char* vl = reinterpret_cast<const char*>(a.v);
+  const int64_t k_row = a.k_ss * EB, v_row = a.v_ss * EB;
+  int blk = t_begin / a.S;  // t_begin is a multiple of S
+  int off = 0;
+  const int64_t bt_row = (int64_t)b * a.bt_sb;
+
+  for (int t0 = t_begin; t0 < t_end; t0 += TOK) {
+    const int64_t phys = load_index(a.bt, a.bt_i64, bt_row + (int64_t)blk * a.bt_sm);
+    const int nvalid = min(TOK, t_end - t0);
+    if (phys >= 0 && phys < a.N) {
+      // Scalar descriptors at this step's first token; per-token offsets go in
+      // the scalar offset, the lane's place in the row in one VGPR.
+      const auto krs = make_rsrc(kl + (phys * a.k_sn + (int64_t)off * a.k_ss) * EB);
+      const auto vrs = make_rsrc(vl + (phys * a.v_sn + (int64_t)off * a.v_ss) * EB);
+      // Tokens past the context re-read the last valid token (never a slot
+      // past the context) and are masked out of the softmax below.
+      uint4 kr[TOK][NL], vr[TOK][NL];
+#pragma unroll
+      for (int t = 0; t < TOK; ++t) {
+        const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * k_row);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          if (FULL || lane_ok) {
+            kr[t][j] = buffer_load16(krs, koff[j], so);
+          } else {
+            kr[t][j] = make_uint4(0u, 0u, 0u, 0u);
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TOK; ++t) {
+        const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * v_row);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          if (FULL || lane_ok) {
+            vr[t][j] = buffer_load16(vrs, voff[j], so);
+          } else {
+            vr[t][j] = make_uint4(0u, 0u, 0u, 0u);
+          }
+        }
+      }
+      // Keep every load of the step ahead of its arithmetic so TOK tokens of
+      // K and V are in flight together.
+      __builtin_amdgcn_sched_barrier(0);
+      float s[TOK];
+      float mb = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < TOK; ++t) {
+        const float d = group_sum<LPH>(q.dot(kr[t])) * a.scale_log2;
+        s[t] = t < nvalid ? d : -INFINITY;
+        mb = fmaxf(mb, s[t]);
+      }
+      const float mn = fmaxf(m, mb);
+      const float alpha = fast_exp2(m - mn);
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+#pragma unroll
+      for (int t = 0; t < TOK; ++t) {
+        const float p = fast_exp2(s[t] - mn);
+        psum += p;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, frag_elem<T>(vr[t], i), acc[i]);
+      }
+      l = l * alpha + psum;
+      m = mn;
+    }
+    off += TOK;
+    if (off >= a.S) {
+      off = 0;
+      ++blk;
+    }
+  }
+
+  if (!lane_ok) return;  // no cross-lane work below
+  if (nparts <= 1) {
+    store_out<T>(a, b, h, sub, acc, l > 0.f ? 1.f / l : 0.f);
+    return;
+  }
+  const size_t pidx = ((size_t)b * a.H + h) * a.max_parts + part;
+  float* wa = a.ws_acc + pidx * D;
+  float4* w0 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, D, 0));
+  float4* w1 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, D, 4));
+  *w0 = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  *w1 = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  if (sub == 0) a.ws_ml[pidx] = make_float2(m, l);
+}
+
+// Combines the partition partials of every (b, h) whose context spans more
+// than one partition.
+template <typename T, int LPH>
+__global__ void __launch_bounds__(64)
+paged_decode_merge(const DecodeArgs a) {
+  constexpr int HPW = 64 / LPH;
+  const int lane = (int)threadIdx.x;
+  const int sub = lane % LPH;
+  const int row = lane / LPH;
+  const int b = (int)blockIdx.y;
+  const int h = (int)blockIdx.x * HPW + row;
+  const int D = a.D;
+  if (h >= a.H || sub * 8 >= D) return;
+  const int ctx = clamp_ctx<T>(a, b);
+  const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  if (nparts <= 1) return;
+
+  const size_t base = ((size_t)b * a.H + h) * a.max_parts;
+  float M = -INFINITY;
+  for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.ws_ml[base + p].x);
+  float L = 0.f;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  if (M != -INFINITY) {
+    for (int p = 0; p < nparts; ++p) {
+      const float2 ml = a.ws_ml[base + p];
+      const float w = fast_exp2(ml.x - M);
+      L = fmaf(w, ml.y, L);
+      const float* wa = a.ws_acc + (base + p) * D;
+      const float4 x0 = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 0));
+      const float4 x1 = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 4));
+      acc[0] = fmaf(w, x0.x, acc[0]);
+      acc[1] = fmaf(w, x0.y, acc[1]);
+      acc[2] = fmaf(w, x0.z, acc[2]);
+      acc[3] = fmaf(w, x0.w, acc[3]);
+      acc[4] = fmaf(w, x1.x, acc[4]);
+      acc[5] = fmaf(w, x1.y, acc[5]);
+      acc[6] = fmaf(w, x1.z, acc[6]);
+      acc[7] = fmaf(w, x1.w, acc[7]);
+    }
+  }
+  store_out<T>(a, b, h, sub, acc, L > 0.f ? 1.f / L : 0.f);
+}
+
+// ----------------------------------------------------------- generic kernel
+// One wavefront per (b, h); lane owns d = lane + 64*j. Any strides, any S.
+constexpr int kGenericMaxD = 512;
+
+template <typename T>
+__global__ void __launch_bounds__(64)
+paged_decode_generic(const DecodeArgs a) {
+  constexpr int NJ = kGenericMaxD / 64;
+  const int lane = (int)threadIdx.x;
+  const int h = (int)blockIdx.x;
+  const int b = (int)blockIdx.y;
+  const int D = a.D;
+  const int ctx = clamp_ctx<T>(a, b);
+
+  const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+  float q[NJ], acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int d = lane + 64 * j;
+    q[j] = d < D ? Elem<T>::load(qrow + (int64_t)d * a.q_sd) : 0.f;
+    acc[j] = 0.f;
+  }
+  const T* kh = reinterpret_cast<const T*>(a.k) + (int64_t)h * a.k_sh;
+  const T* vh = reinterpret_cast<const T*>(a.v) + (int64_t)h * a.v_sh;
+  const int64_t bt_row = (int64_t)b * a.bt_sb;
+  float m = -INFINITY, l = 0.f;
+  int blk = 0, off = 0;
+  int64_t phys = 0;
+  for (int t = 0; t < ctx; ++t) {
+    if (off == 0) phys = load_index(a.bt, a.bt_i64, bt_row + (int64_t)blk * a.bt_sm);
+    if (phys >= 0 && phys < a.N) {
+      const T* kt = kh + phys * a.k_sn + (int64_t)off * a.k_ss;
+      const T* vt = vh + phys * a.v_sn + (int64_t)off * a.v_ss;
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = lane + 64 * j;
+        if (d < D) part = fmaf(q[j], Elem<T>::load(kt + (int64_t)d * a.k_sd), part);
+      }
+      const float s = wave_sum(part) * a.scale_log2;
+      const float mn = fmaxf(m, s);
+      const float alpha = fast_exp2(m - mn);
+      const float p = fast_exp2(s - mn);
+      l = l * alpha + p;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = lane + 64 * j;
+        const float v = d < D ? Elem<T>::load(vt + (int64_t)d * a.v_sd) : 0.f;
+        acc[j] = fmaf(p, v, acc[j] * alpha);
+      }
+      m = mn;
+    }
+    if (++off == a.S) {
+      off = 0;
+      ++blk;
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) Elem<T>::store(orow + (int64_t)d * a.o_sd, acc[j] * inv);
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+static hipError_t launch(const void* fn, dim3 grid, dim3 block, const DecodeArgs& a,
+                         hipStream_t stream) {
+  void* args[] = {const_cast<DecodeArgs*>(&a)};
+  return hipLaunchKernel(fn, grid, block, args, 0, stream);
+}
+
+template <typename T, int LPH, int TOK>
+static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_t stream) {
+  constexpr int HPW = 64 / LPH;
+  const dim3 grid((unsigned)((a.H + HPW - 1) / HPW), (unsigned)a.max_parts, (unsigned)a.B);
+  const void* fn = full ? reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, true>)
+                        : reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, false>);
+  hipError_t e = launch(fn, grid, dim3(64), a, stream);
+  if (e != hipSuccess || a.max_parts <= 1) return e;
+  const dim3 mgrid((unsigned)((a.H + HPW - 1) / HPW), (unsigned)a.B);
+  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH>), mgrid, dim3(64), a,
+                stream);
+}
+
+template <typename T, int LPH>
+static hipError_t launch_fast_lph(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+  if constexpr (sizeof(T) == 2) {
+    if (p.tokens_per_step == 16) return launch_fast_lph_tok<T, LPH, 16>(a, p.full_lanes, stream);
+  }
+  if (p.tokens_per_step == 8) return launch_fast_lph_tok<T, LPH, 8>(a, p.full_lanes, stream);
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+static hipError_t launch_fast(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+  switch (p.lanes_per_head) {
+    case 4: return launch_fast_lph<T, 4>(a, p, stream);
+    case 8: return launch_fast_lph<T, 8>(a, p, stream);
+    case 16: return launch_fast_lph<T, 16>(a, p, stream);
+    case 32: return launch_fast_lph<T, 32>(a, p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename T>
+static hipError_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
+  return launch(reinterpret_cast<const void*>(&paged_decode_generic<T>),
+                dim3((unsigned)a.H, (unsigned)a.B), dim3(64), a, stream);
+}
+
+hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan& plan,
+                               hipStream_t stream) {
+  if (plan.path == DecodePath::kFast) {
+    if (dtype == MGI_BF16) return launch_fast<bf16_t>(a, plan, stream);
+    if (dtype == MGI_F32) return launch_fast<float>(a, plan, stream);
+    return hipErrorInvalidValue;
+  }
+  if (dtype == MGI_BF16) return launch_generic<bf16_t>(a, stream);
+  if (dtype == MGI_F32) return launch_generic<float>(a, stream);
+  if (dtype == MGI_F16) return launch_generic<f16_t>(a, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mgi

@@ -1,0 +1,114 @@
+"""libminivllm_hip.so loads, exports every symbol include/minivllm_hip.h declares,
+and rejects bad arguments on the host (no device work is issued by these
+calls: validation returns before any HIP call)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from minivllm import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "minivllm_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mgi_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    assert declared_symbols() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.mgi_abi_version() == 100
+
+
+def test_split_tokens_and_workspace_sizes():
+    lib = _native.lib()
+    # decode microbench shape: M = 256 columns of S = 16 -> 16 partitions of 256
+    assert lib.mgi_paged_decode_split_tokens(64, 32, 128, 16, 256, 0) == 256
+    n = 64 * 32 * 16
+    acc = n * 128 * 4
+    assert lib.mgi_paged_decode_workspace_bytes(64, 32, 128, 16, 256, 0) == ((acc + 255) // 256) * 256 + n * 8
+    # a table that fits one partition needs no workspace
+    assert lib.mgi_paged_decode_workspace_bytes(4, 8, 32, 16, 4, 0) == 0
+    for S, M, req in [(16, 8192, 0), (8, 100, 0), (12, 77, 100), (16, 256, 1), (16, 256, 5000)]:
+        P = lib.mgi_paged_decode_split_tokens(1, 1, 128, S, M, req)
+        assert P % S == 0 or P == M * S
+        assert 0 < P <= M * S
+        assert (M * S + P - 1) // P <= 65535
+
+
+def _i64(*xs):
+    return (ctypes.c_int64 * len(xs))(*xs)
+
+
+def test_paged_decode_rejects_bad_arguments_on_host():
+    lib = _native.lib()
+    st3, st5, st2 = _i64(1, 1, 1), _i64(1, 1, 1, 1, 1), _i64(1, 1)
+    fake = 0x1000  # never dereferenced: every call below fails validation first
+
+    def call(**kw):
+        a = dict(out=fake, q=fake, k=fake, v=fake, dtype=_native.MGI_F32, bt=fake, bt_it=1, cl=fake,
+                 cl_it=1, B=1, H=1, D=8, S=16, N=4, M=1, L=1, layer=0, scale=0.5)
+        a.update(kw)
+        return lib.mgi_paged_decode(a["out"], st3, a["q"], st3, a["k"], a["v"], st5, st5, a["dtype"],
+                                    a["bt"], st2, a["bt_it"], a["cl"], 1, a["cl_it"], a["B"], a["H"],
+                                    a["D"], a["S"], a["N"], a["M"], a["L"], a["layer"], a["scale"], 0,
+                                    None, 0, None)
+
+    cases = [
+        (dict(q=None), "null tensor pointer"),
+        (dict(B=0), "q dimensions must be nonzero"),
+        (dict(M=0), "at least one block column"),
+        (dict(layer=1), "layer_idx outside KV pool"),
+        (dict(dtype=7), "unknown dtype"),
+        (dict(bt_it=5), "int32 or int64"),
+        (dict(scale=float("nan")), "scale must be finite"),
+        (dict(D=1024), "head_dim larger than 512"),
+    ]
+    for kw, msg in cases:
+        assert call(**kw) == _native.MGI_EINVAL or call(**kw) == _native.MGI_EUNSUPPORTED, kw
+        assert msg in lib.mgi_last_error().decode(), (kw, lib.mgi_last_error())
+
+
+def test_kv_append_rejects_bad_arguments_on_host():
+    lib = _native.lib()
+    st3, st5 = _i64(1, 1, 1), _i64(1, 1, 1, 1, 1)
+    fake = 0x1000
+
+    def call(T=1, layer=0, pool_dtype=_native.MGI_BF16, new_dtype=_native.MGI_BF16, k_pool=fake):
+        return lib.mgi_kv_append(k_pool, fake, st5, st5, pool_dtype, fake, fake, st3, st3, new_dtype,
+                                 fake, 1, _native.MGI_I64, T, 2, 8, 16, 4, 1, layer, None)
+
+    assert call(T=0) == _native.MGI_OK  # nothing to do: no launch
+    assert call(T=-1) == _native.MGI_EINVAL
+    assert call(layer=3) == _native.MGI_EINVAL
+    assert call(k_pool=None) == _native.MGI_EINVAL
+    assert call(pool_dtype=_native.MGI_BF16, new_dtype=_native.MGI_F16) == _native.MGI_EUNSUPPORTED
+    assert "f32" in lib.mgi_last_error().decode()
+
+
+def test_status_mapping_to_python_exceptions():
+    lib = _native.lib()
+    st3, st5 = _i64(1, 1, 1), _i64(1, 1, 1, 1, 1)
+    lib.mgi_kv_append(None, None, st5, st5, 0, None, None, st3, st3, 0, None, 1, 1, 1, 1, 1, 1, 1, 1,
+                      0, None)
+    with pytest.raises(ValueError, match="null tensor pointer"):
+        _native.check(_native.MGI_EINVAL)
+    with pytest.raises(RuntimeError):
+        _native.check(_native.MGI_ELAUNCH)
+
+
+def test_dtype_codes_cover_supported_types():
+    assert set(_native.DTYPE_CODES) == {torch.float32, torch.bfloat16, torch.float16}
+    assert set(_native.ITYPE_CODES) == {torch.int32, torch.int64}

@@ -1,0 +1,240 @@
+"""Parity of the HIP paged decode attention with the CPU oracle (MI355X).
+
+Tolerances (north star): fp32 within 1e-5 (rtol and atol, as the reference
+tests pair them, tests/test_paged_attention.py:32); bf16 within 2e-2 against
+the oracle evaluated in double on the same bf16 inputs; large logits 5e-4
+(tests/test_triton_paged_decode.py:66-71). Small cases check every element;
+benchmark-size cases check the C oracle on the drawn workload plus
+size-independent properties: block-placement invariance (bit-exact),
+partition-size invariance, single-token contexts (bit-exact) and finiteness
+with NaN in every slot past a context.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import _fixtures as fx
+from minivllm import hip_paged_decode as hpd
+from minivllm.kv_block_pool import KVBlockPool
+from oracle import c_oracle
+from oracle import paged_decode as ora
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+F32_TOL = dict(rtol=1e-5, atol=1e-5)
+BF16_TOL = dict(rtol=2e-2, atol=2e-2)
+
+
+def tol_for(dtype):
+    return F32_TOL if dtype == torch.float32 else BF16_TOL
+
+
+def hip(q, pool, tables, lens, layer, **kw):
+    print(f"  hip decode B={q.shape[0]} H={q.shape[1]} D={q.shape[2]} S={pool.block_size} "
+          f"dtype={q.dtype} kw={kw}", flush=True)
+    with torch.inference_mode():
+        out = hpd.paged_attention_batch_hip(q.to(DEV), pool, tables.to(DEV), lens.to(DEV), layer, **kw)
+    torch.cuda.synchronize()
+    assert out.dtype == q.dtype and tuple(out.shape) == tuple(q.shape)
+    return out.float().cpu().numpy()
+
+
+def oracle_args(q, pool, tables, lens, layer):
+    return (fx.to_numpy(q), fx.to_numpy(pool.k), fx.to_numpy(pool.v), tables.cpu().numpy(),
+            lens.cpu().numpy(), layer)
+
+
+# ------------------------------------------------ reference test fixtures
+
+@pytest.mark.parametrize("case", [0, 1, 2])
+def test_reference_unit_cases(case):
+    pool, _, cases = fx.reference_case_2026()
+    _, q, tables, lens = cases[case]
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, 0)
+    want = ora.paged_attention_online_v1(*oracle_args(q, pool, tables, lens, 0))
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, **F32_TOL)
+
+
+@pytest.mark.parametrize("make", [fx.padding_case_11, fx.probe_case_2026])
+def test_nan_pool_cases(make):
+    pool, q, tables, lens = make()
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, 0)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, 0)), **F32_TOL)
+
+
+@pytest.mark.parametrize("bs,length,batch,dim", [
+    (16, 1, 1, 32), (16, 15, 2, 32), (16, 16, 2, 32), (16, 17, 4, 32), (16, 65, 4, 32),
+    (16, 129, 4, 32), (16, 257, 2, 32), (8, 37, 3, 16), (32, 129, 3, 64), (16, 33, 2, 48)])
+def test_kernel_matches_oracle_reference_grid(bs, length, batch, dim):
+    """The GPU grid of tests/test_triton_paged_decode.py:51-64 (8 heads, scale 0.3)."""
+    q, pool, tables, lens, layer = fx.build_case(batch, length, 8, dim, bs, "mixed", scale=0.3)
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)), **F32_TOL)
+
+
+def test_large_logits_stable():
+    q, pool, tables, lens, layer = fx.build_case(2, 65, 4, 32, 16, "mixed", scale=8.0)
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)),
+                               rtol=5e-4, atol=5e-4)
+
+
+# ------------------------------------------------------- shape / path sweep
+
+def _small_case(B, H, D, S, ctx, dtype, seed, N=None, layers=2, layer=1):
+    g = torch.Generator().manual_seed(seed)
+    nblk = [(c + S - 1) // S for c in ctx]
+    N = N or sum(nblk) + 5
+    M = max(max(nblk), 1)
+    pool = KVBlockPool(layers, N, S, H, D, dtype=dtype)
+    pool.k.copy_(torch.randn(pool.k.shape, generator=g).to(dtype))
+    pool.v.copy_(torch.randn(pool.v.shape, generator=g).to(dtype))
+    perm = torch.randperm(N, generator=g)
+    tables = torch.full((B, M), -1, dtype=torch.int64)
+    used = 0
+    for b in range(B):
+        tables[b, : nblk[b]] = perm[used: used + nblk[b]]
+        # NaN past the context in the last block
+        if ctx[b] % S:
+            last = int(perm[used + nblk[b] - 1])
+            pool.k[layer, last, ctx[b] % S:] = float("nan")
+            pool.v[layer, last, ctx[b] % S:] = float("nan")
+        used += nblk[b]
+    q = torch.randn((B, H, D), generator=g).to(dtype)
+    return q, pool, tables, torch.tensor(ctx, dtype=torch.int64), layer
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("S,H", [(16, 32), (8, 3), (32, 5)])
+@pytest.mark.parametrize("split", [0, 16, 48, 256])
+def test_fast_path_shapes(dtype, D, S, H, split):
+    ctx = [1, S - 1, S, 3 * S + 1, 300, 513]
+    q, pool, tables, lens, layer = _small_case(len(ctx), H, D, S, ctx, dtype, seed=D + S + H + split)
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer, split_tokens=split)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)),
+                               **tol_for(dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,S", [(4, 4), (12, 5), (100, 16), (8, 1), (300, 3)])
+def test_generic_path_shapes(dtype, D, S):
+    ctx = [1, 7, 40, 65]
+    q, pool, tables, lens, layer = _small_case(len(ctx), 3, D, S, ctx, dtype, seed=D * 7 + S)
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
+    assert np.isfinite(got).all()
+    tol = F32_TOL if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+    np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)), **tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_int32_indices_and_strided_q(dtype):
+    ctx = [5, 77, 190]
+    q, pool, tables, lens, layer = _small_case(3, 8, 128, 16, ctx, dtype, seed=11)
+    wide = torch.randn(3, 8, 256).to(dtype)
+    wide[..., ::2] = q
+    q_strided = wide[..., ::2]
+    assert q_strided.stride(-1) == 2
+    got = hip(q_strided, fx.pool_to_device(pool, DEV), tables.int(), lens.int(), layer, split_tokens=64)
+    np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)),
+                               **tol_for(dtype))
+
+
+def test_zero_context_row_gives_zeros():
+    q, pool, tables, lens, layer = _small_case(3, 4, 64, 16, [9, 40, 3], torch.float32, seed=5)
+    lens[1] = 0
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
+    assert (got[1] == 0).all()
+    keep = [0, 2]
+    want = ora.dense_gold(*oracle_args(q[keep], pool, tables[keep], lens[keep], layer))
+    np.testing.assert_allclose(got[keep], want, **F32_TOL)
+
+
+def test_out_of_range_table_entries_inside_context_are_masked():
+    q, pool, tables, lens, layer = _small_case(2, 4, 128, 16, [64, 64], torch.float32, seed=9)
+    bad = tables.clone()
+    bad[0, 1] = pool.num_blocks + 3
+    bad[1, 2] = -1
+    got = hip(q, fx.pool_to_device(pool, DEV), bad, lens, layer, split_tokens=32)
+    want = c_oracle.paged_decode(*oracle_args(q, pool, bad, lens, layer))
+    np.testing.assert_allclose(got, want, **F32_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_single_token_context_returns_value_row_exactly(dtype):
+    q, pool, tables, lens, layer = _small_case(4, 32, 128, 16, [1, 1, 1, 1], dtype, seed=3)
+    dpool = fx.pool_to_device(pool, DEV)
+    with torch.inference_mode():
+        out = hpd.paged_attention_batch_hip(q.to(DEV), dpool, tables.to(DEV), lens.to(DEV), layer)
+    want = dpool.v[layer, tables[:, 0].to(DEV), 0]
+    assert torch.equal(out.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                       want.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
+
+
+# ------------------------------------------------- benchmark-size parity
+
+def _check_against_c_oracle(w, dtype, seqs=None):
+    with torch.inference_mode():
+        out = hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    if seqs is not None:
+        sub = fx.DecodeWorkload(w.q[seqs], w.pool, w.tables[seqs], w.ctx[seqs], w.layer, w.meta)
+        got = got[seqs]
+    else:
+        sub = w
+    want = c_oracle.paged_decode(*sub.compact_host(), threads=fx.oracle_threads())
+    np.testing.assert_allclose(got, want, **tol_for(dtype))
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_microbench_shape_matches_oracle(dtype):
+    """B=64, H=32, D=128, S=16, ctx ~ U[512, 4096], 20k-block permuted pool."""
+    print(f"  workload B=64 H=32 D=128 ctx U[512,4096] N=20000 {dtype}", flush=True)
+    w = fx.make_decode_workload(64, 32, 128, 16, 20000, 512, 4096, dtype, DEV, seed=0)
+    _check_against_c_oracle(w, dtype)
+
+
+def test_decode_microbench_invariances():
+    w = fx.make_decode_workload(64, 32, 128, 16, 20000, 512, 4096, torch.float32, DEV, seed=1)
+    with torch.inference_mode():
+        base = hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer)
+        # partition size only changes the order of the merge
+        for split in (64, 512, 1024, 4096):
+            print(f"  split_tokens={split}", flush=True)
+            other = hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer,
+                                                  split_tokens=split)
+            torch.testing.assert_close(other, base, **F32_TOL)
+        # physical placement of blocks does not enter the arithmetic: bit-exact
+        g = torch.Generator(device=DEV).manual_seed(5)
+        perm = torch.randperm(w.pool.num_blocks, generator=g, device=DEV)
+        inv = torch.argsort(perm)
+        moved = KVBlockPool(1, w.pool.num_blocks, 16, 32, 128, device=DEV, dtype=torch.float32)
+        moved.k.copy_(w.pool.k[:, perm])
+        moved.v.copy_(w.pool.v[:, perm])
+        tables2 = torch.where(w.tables >= 0, inv[w.tables.clamp(min=0)], w.tables)
+        again = hpd.paged_attention_batch_hip(w.q, moved, tables2, w.ctx, w.layer)
+    assert torch.equal(again.view(torch.int32), base.view(torch.int32))
+
+
+def test_long_context_split_decode():
+    """B=8, H=32, D=128, bf16, ctx ~ U[32768, 131072] over a 65536-block pool."""
+    print("  workload B=8 ctx U[32768,131072] N=65536 bf16", flush=True)
+    w = fx.make_decode_workload(8, 32, 128, 16, 65536, 32768, 131072, torch.bfloat16, DEV, seed=0,
+                                poison=False)
+    base = _check_against_c_oracle(w, torch.bfloat16, seqs=[0, 5])
+    with torch.inference_mode():
+        for split in (256, 512, 1024, 2048):
+            print(f"  split_tokens={split}", flush=True)
+            other = hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer,
+                                                  split_tokens=split)
+            torch.testing.assert_close(other.float(), base.float(), **BF16_TOL)
