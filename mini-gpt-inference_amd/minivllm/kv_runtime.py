@@ -1,0 +1,44 @@
+"""Per-call execution contexts (minivllm/kv_runtime.py:7-55)."""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from .block_manager import BlockManager
+from .kv_block_pool import KVBlockPool
+from .sequence import SequenceState
+
+
+@dataclass
+class KVRuntimeContext:
+    """One-token serial decode of one layer."""
+    seq_state: SequenceState
+    block_manager: BlockManager
+    kv_pool: KVBlockPool
+    layer_idx: int
+    logical_pos: int
+    context_length: int
+    physical_block: int
+    block_offset: int
+    physical_slot: int
+
+
+@dataclass
+class PrefillRuntimeContext:
+    """Whole-prompt prefill of one layer."""
+    seq_state: SequenceState
+    kv_pool: KVBlockPool
+    layer_idx: int
+    start_pos: int
+    context_length: int
+    slot_mapping: list[int]
+
+
+@dataclass
+class PrefillChunkContext:
+    """One prefill chunk [start_pos, start_pos + num_tokens) of one layer."""
+    seq_state: SequenceState
+    kv_pool: KVBlockPool
+    layer_idx: int
+    start_pos: int
+    num_tokens: int
+    slot_mapping: list[int]
