@@ -45,6 +45,9 @@ def parse_args():
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--no-extras", action="store_true", help="skip the other workload shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="also run a device-to-device copy of this many MiB (3 times) so rocprof "
+                         "counters can be scaled by a kernel of known traffic")
     return ap.parse_args()
 
 
@@ -102,6 +105,17 @@ def append_line(steps, warmup, dev):
     nbytes = n_valid * H * D * 2 * 2 * 2 + B * 8
     return {"us": round(ms * 1e3, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "valid_rows": n_valid,
             "alg_bytes": nbytes, "note": "launch-latency bound; working set is cache resident"}
+
+
+def copy_line(mib: int, dev, reps: int = 3):
+    """Device-to-device copy of `mib` MiB: read + write bandwidth, the sanity ceiling."""
+    import torch
+
+    src = torch.empty(mib * (1 << 20), dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    ms = time_steps(lambda: dst.copy_(src), reps, 1)
+    return {"mib": mib, "ms": round(ms, 4), "gbps_read_plus_write": round(2 * src.numel() / (ms * 1e-3) / 1e9, 1)}
 
 
 def cpu_baseline(w):
@@ -184,7 +198,13 @@ def main() -> None:
             log(f"extra longctx: {extras['longctx_bf16_B8_ctx32k-128k']}")
             extras["kv_append_bf16_B256"] = append_line(max(20, args.steps), 5, dev)
             log(f"extra append: {extras['kv_append_bf16_B256']}")
+            extras["d2d_copy_4GiB"] = copy_line(4096, dev, reps=5)
+            log(f"extra copy: {extras['d2d_copy_4GiB']}")
             torch.cuda.empty_cache()
+
+        if args.calibrate_copy_mib:
+            extras["copy_calibration"] = copy_line(args.calibrate_copy_mib, dev, reps=3)
+            log(f"copy calibration: {extras['copy_calibration']}")
 
         cpu = None
         if not args.no_cpu_baseline:

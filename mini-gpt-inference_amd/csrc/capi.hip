@@ -5,6 +5,7 @@
 // nothing here reads device memory or synchronises the stream.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <string>
 
 #include "mgi_internal.h"
@@ -36,19 +37,17 @@ constexpr int64_t kWorkspaceAlign = 256;
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// Partition size in tokens: a multiple of S, one partition when the whole
-// table fits, and at most kMaxGridYZ partitions per sequence.
+// Blocks one partition of the fast kernel may span (its block-table entries
+// live in two VGPRs of the wavefront).
+constexpr int64_t kMaxBlocksPerPart = 128;
+
+// Partition size in tokens: a multiple of S, at most kMaxBlocksPerPart
+// blocks, and the whole table when that fits in one partition.
 int64_t split_tokens_for(int64_t S, int64_t M, int64_t requested) {
   const int64_t max_ctx = M * S;
-  int64_t P = requested;
-  if (P <= 0) {
-    P = 256;
-    while (P * 1024 < max_ctx) P *= 2;  // keep <= 1024 partitions per sequence
-  }
-  P = round_up(P, S);
-  while ((max_ctx + P - 1) / P > kMaxGridYZ) P = round_up(P * 2, S);
-  if (P >= max_ctx) P = max_ctx;
-  return P;
+  int64_t P = requested > 0 ? requested : 512;
+  P = std::min(round_up(P, S), kMaxBlocksPerPart * S);
+  return std::min(P, max_ctx);
 }
 
 struct WorkspaceLayout {
@@ -66,6 +65,18 @@ WorkspaceLayout workspace_layout(int64_t B, int64_t H, int64_t D, int64_t S, int
   w.ml_offset = (size_t)round_up((int64_t)w.acc_bytes, kWorkspaceAlign);
   w.total = w.ml_offset + (size_t)(n * 8);
   return w;
+}
+
+// Tokens loaded per pipeline stage of the fast kernel: 8 for bf16 and 4 for
+// f32 (16 KiB of K+V per stage and wavefront at head_dim 128), or the largest
+// of those S allows. MINIVLLM_HIP_TOKENS_PER_STEP (4, 8, or 16 for bf16)
+// overrides the choice when S allows it (tuning).
+int tokens_per_step_override() {
+  static const int v = [] {
+    const char* e = std::getenv("MINIVLLM_HIP_TOKENS_PER_STEP");
+    return e ? std::atoi(e) : 0;
+  }();
+  return v;
 }
 
 int next_pow2_at_least4(int64_t x) {
@@ -124,6 +135,8 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
       !nonneg(v_pool_strides, 5) || !nonneg(bt_strides, 2) || cl_stride < 0)
     return fail(MGI_EINVAL, "strides must be non-negative");
   if (B > kMaxGridYZ) return fail(MGI_EUNSUPPORTED, "batch larger than 65535");
+  if (M > kMaxGridYZ * kMaxBlocksPerPart)
+    return fail(MGI_EUNSUPPORTED, "block table wider than 65535 partitions");
   if (M * S >= (int64_t(1) << 31)) return fail(MGI_EUNSUPPORTED, "M*S must be < 2^31");
   if (D > 512) return fail(MGI_EUNSUPPORTED, "head_dim larger than 512");
 
@@ -147,8 +160,14 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
       row_span < (int64_t(1) << 31) &&
       std::max(k_pool_strides[2], v_pool_strides[2]) * eb * S < (int64_t(1) << 31)) {
     int tok = 0;
-    if (dtype == MGI_BF16 && S % 16 == 0) tok = 16;
-    else if (S % 8 == 0) tok = 8;
+    const int want = tokens_per_step_override();
+    const int def = dtype == MGI_BF16 ? 8 : 4;
+    for (int t : {want, def, 8, 4}) {
+      if (t > 0 && (t == 4 || t == 8 || (t == 16 && dtype == MGI_BF16)) && S % t == 0) {
+        tok = t;
+        break;
+      }
+    }
     if (tok) {
       plan.path = DecodePath::kFast;
       plan.tokens_per_step = tok;
@@ -199,8 +218,6 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
     if (!aligned16(workspace)) return fail(MGI_EINVAL, "workspace must be 16-byte aligned");
     a.ws_acc = static_cast<float*>(workspace);
     a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + ws.ml_offset);
-  } else {
-    a.part_tokens = (int)(M * S);  // one partition covers every context
   }
 
   const hipError_t e = launch_paged_decode(a, dtype, plan, static_cast<hipStream_t>(stream));

@@ -87,24 +87,37 @@ __device__ __forceinline__ float swizzle_xor16(float x) {
       float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
 }
 
-// Sum over aligned groups of G lanes (G in {1,2,4,8,16,32}); every lane of
-// the group receives the full sum. Within a 16-lane DPP row the partner
+struct SumOp {
+  __device__ static float apply(float x, float y) { return x + y; }
+};
+struct MaxOp {
+  __device__ static float apply(float x, float y) { return fmaxf(x, y); }
+};
+
+// Reduction over aligned groups of G lanes (G in {1,2,4,8,16,32}); every
+// lane of the group receives the result. Within a 16-lane DPP row the partner
 // patterns mirror, half-mirror, quad xor2, quad xor1 combine all 16 inputs.
-template <int G>
-__device__ __forceinline__ float group_sum(float x) {
-  if constexpr (G >= 16) x += dpp<DPP_ROW_MIRROR>(x);
-  if constexpr (G >= 8) x += dpp<DPP_ROW_HALF_MIRROR>(x);
-  if constexpr (G >= 4) x += dpp<DPP_QUAD_XOR2>(x);
-  if constexpr (G >= 2) x += dpp<DPP_QUAD_XOR1>(x);
-  if constexpr (G >= 32) x += swizzle_xor16(x);
+template <int G, typename Op = SumOp>
+__device__ __forceinline__ float group_reduce(float x) {
+  if constexpr (G >= 16) x = Op::apply(x, dpp<DPP_ROW_MIRROR>(x));
+  if constexpr (G >= 8) x = Op::apply(x, dpp<DPP_ROW_HALF_MIRROR>(x));
+  if constexpr (G >= 4) x = Op::apply(x, dpp<DPP_QUAD_XOR2>(x));
+  if constexpr (G >= 2) x = Op::apply(x, dpp<DPP_QUAD_XOR1>(x));
+  if constexpr (G >= 32) x = Op::apply(x, swizzle_xor16(x));
   return x;
 }
 
-// Full 64-lane sum, result in every lane (slow path helper).
+template <int G>
+__device__ __forceinline__ float group_sum(float x) { return group_reduce<G, SumOp>(x); }
+
+// Full 64-lane reductions, result in every lane.
 __device__ __forceinline__ float wave_sum(float x) {
-  x = group_sum<32>(x);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  x = group_reduce<32, SumOp>(x);
+  return x + __shfl_xor(x, 32, 64);
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = group_reduce<32, MaxOp>(x);
+  return fmaxf(x, __shfl_xor(x, 32, 64));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -127,6 +127,19 @@ __device__ __forceinline__ void store_out(const DecodeArgs& a, int b, int h, int
 }
 
 // ------------------------------------------------------------- fast kernel
+
+// Largest number of S-token blocks one partition may span: the partition's
+// block-table entries are held one per lane in two VGPRs (the host caps the
+// partition size at kMaxBlocksPerPart * S).
+constexpr int kMaxBlocksPerPart = 128;
+
+// Raw K and V fragments of TOK consecutive tokens of one block.
+template <typename T, int TOK>
+struct Step {
+  uint4 k[TOK][Layout<T>::kLoads];
+  uint4 v[TOK][Layout<T>::kLoads];
+};
+
 template <typename T, int LPH, int TOK, bool FULL>
 __global__ void __launch_bounds__(64)
 paged_decode_fast(const DecodeArgs a) {
@@ -140,12 +153,32 @@ paged_decode_fast(const DecodeArgs a) {
   const int part = (int)blockIdx.y;
   const int h = (int)blockIdx.x * HPW + row;
   const int D = a.D;
+  const int S = a.S;
   const bool lane_ok = FULL || (h < a.H && sub * 8 < D);
 
   const int ctx = clamp_ctx<T>(a, b);
   const int P = a.part_tokens;
   const int nparts = (ctx + P - 1) / P;
   if (part >= (nparts > 0 ? nparts : 1)) return;  // uniform over the wave
+
+  const int t_begin = part * P;  // a multiple of S
+  const int t_end = min(ctx, t_begin + P);
+  const int nsteps = (t_end - t_begin + TOK - 1) / TOK;
+  const int blk0 = t_begin / S;
+  const int nblk = (t_end - t_begin + S - 1) / S;  // <= kMaxBlocksPerPart
+
+  // Lane j holds this partition's physical block ids j (phys_lo) and 64 + j
+  // (phys_hi); -1 marks an out-of-range entry (masked) or no block.
+  int phys_lo = -1, phys_hi = -1;
+  const int64_t bt_row = (int64_t)b * a.bt_sb;
+  if (lane < nblk) {
+    const int64_t e = load_index(a.bt, a.bt_i64, bt_row + (int64_t)(blk0 + lane) * a.bt_sm);
+    phys_lo = (e >= 0 && e < a.N) ? (int)e : -1;
+  }
+  if (64 + lane < nblk) {
+    const int64_t e = load_index(a.bt, a.bt_i64, bt_row + (int64_t)(blk0 + 64 + lane) * a.bt_sm);
+    phys_hi = (e >= 0 && e < a.N) ? (int)e : -1;
+  }
 
   QFrag<T> q;
   q.zero();
@@ -160,86 +193,93 @@ paged_decode_fast(const DecodeArgs a) {
     koff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.k_sh + Layout<T>::load_off(sub, D, j)) * EB) : 0u;
     voff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.v_sh + Layout<T>::load_off(sub, D, j)) * EB) : 0u;
   }
+  const char* kl = reinterpret_cast<const char*>(a.k);
+  const char* vl = reinterpret_cast<const char*>(a.v);
+  const int64_t k_row = a.k_ss * EB, v_row = a.v_ss * EB;
+  const int steps_per_blk = S / TOK;
+
+  // Issues the K/V loads of step s (clamped to the last step: a step past the
+  // partition re-reads that step's lines, which are cache-resident, so every
+  // iteration issues the same number of loads). Returns the number of valid
+  // tokens of step s (0 past the partition or for a masked block).
+  auto issue = [&](int s, Step<T, TOK>& st) -> int {
+    const int sc = s < nsteps ? s : nsteps - 1;
+    const int rel = sc / steps_per_blk;
+    const int off = (sc - rel * steps_per_blk) * TOK;
+    const int phys = rel < 64 ? __builtin_amdgcn_readlane(phys_lo, rel)
+                              : __builtin_amdgcn_readlane(phys_hi, rel - 64);
+    const int nvalid = min(TOK, t_end - (t_begin + sc * TOK));
+    const int64_t pb = phys >= 0 ? phys : 0;  // a masked block is read from block 0, never used
+    const auto krs = make_rsrc(kl + (pb * a.k_sn + (int64_t)off * a.k_ss) * EB);
+    const auto vrs = make_rsrc(vl + (pb * a.v_sn + (int64_t)off * a.v_ss) * EB);
+    // Tokens past the context re-read the last valid token (never a slot
+    // past the context) and are masked out of the softmax.
+#pragma unroll
+    for (int t = 0; t < TOK; ++t) {
+      const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * k_row);
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        if (FULL || lane_ok) st.k[t][j] = buffer_load16(krs, koff[j], so);
+        else st.k[t][j] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TOK; ++t) {
+      const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * v_row);
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        if (FULL || lane_ok) st.v[t][j] = buffer_load16(vrs, voff[j], so);
+        else st.v[t][j] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+    return (s < nsteps && phys >= 0) ? nvalid : 0;
+  };
 
   float m = -INFINITY, l = 0.f;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
 
-  const int t_begin = part * P;
-  const int t_end = min(ctx, t_begin + P);
-  const char* kl = reinterpret_cast<const char*>(a.k);
-  const char* vl = reinterpret_cast<const char*>(a.v);
-  const int64_t k_row = a.k_ss * EB, v_row = a.v_ss * EB;
-  int blk = t_begin / a.S;  // t_begin is a multiple of S
-  int off = 0;
-  const int64_t bt_row = (int64_t)b * a.bt_sb;
-
-  for (int t0 = t_begin; t0 < t_end; t0 += TOK) {
-    const int64_t phys = load_index(a.bt, a.bt_i64, bt_row + (int64_t)blk * a.bt_sm);
-    const int nvalid = min(TOK, t_end - t0);
-    if (phys >= 0 && phys < a.N) {
-      // Scalar descriptors at this step's first token; per-token offsets go in
-      // the scalar offset, the lane's place in the row in one VGPR.
-      const auto krs = make_rsrc(kl + (phys * a.k_sn + (int64_t)off * a.k_ss) * EB);
-      const auto vrs = make_rsrc(vl + (phys * a.v_sn + (int64_t)off * a.v_ss) * EB);
-      // Tokens past the context re-read the last valid token (never a slot
-      // past the context) and are masked out of the softmax below.
-      uint4 kr[TOK][NL], vr[TOK][NL];
+  // Folds one step into the online softmax (scores in the log2 domain).
+  auto consume = [&](const Step<T, TOK>& st, int nvalid) {
+    float s[TOK];
+    float mb = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < TOK; ++t) {
-        const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * k_row);
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-          if (FULL || lane_ok) {
-            kr[t][j] = buffer_load16(krs, koff[j], so);
-          } else {
-            kr[t][j] = make_uint4(0u, 0u, 0u, 0u);
-          }
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < TOK; ++t) {
-        const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * v_row);
-#pragma unroll
-        for (int j = 0; j < NL; ++j) {
-          if (FULL || lane_ok) {
-            vr[t][j] = buffer_load16(vrs, voff[j], so);
-          } else {
-            vr[t][j] = make_uint4(0u, 0u, 0u, 0u);
-          }
-        }
-      }
-      // Keep every load of the step ahead of its arithmetic so TOK tokens of
-      // K and V are in flight together.
-      __builtin_amdgcn_sched_barrier(0);
-      float s[TOK];
-      float mb = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < TOK; ++t) {
-        const float d = group_sum<LPH>(q.dot(kr[t])) * a.scale_log2;
-        s[t] = t < nvalid ? d : -INFINITY;
-        mb = fmaxf(mb, s[t]);
-      }
-      const float mn = fmaxf(m, mb);
-      const float alpha = fast_exp2(m - mn);
-      float psum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-#pragma unroll
-      for (int t = 0; t < TOK; ++t) {
-        const float p = fast_exp2(s[t] - mn);
-        psum += p;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, frag_elem<T>(vr[t], i), acc[i]);
-      }
-      l = l * alpha + psum;
-      m = mn;
+    for (int t = 0; t < TOK; ++t) {
+      // Rounded multiply (never fused into the exponent's subtraction), so the
+      // largest score minus the running max is exactly 0 and its weight is 1.
+      const float d = __fmul_rn(group_sum<LPH>(q.dot(st.k[t])), a.scale_log2);
+      s[t] = t < nvalid ? d : -INFINITY;
+      mb = fmaxf(mb, s[t]);
     }
-    off += TOK;
-    if (off >= a.S) {
-      off = 0;
-      ++blk;
+    const float mn = fmaxf(m, mb);
+    const float alpha = fast_exp2(m - mn);
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int t = 0; t < TOK; ++t) {
+      const float p = fast_exp2(s[t] - mn);
+      psum += p;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, frag_elem<T>(st.v[t], i), acc[i]);
+    }
+    l = l * alpha + psum;
+    m = mn;
+  };
+
+  // Two-deep software pipeline: the loads of step s+1 are in flight while
+  // step s is folded in.
+  if (nsteps > 0) {
+    Step<T, TOK> A, B;
+    int nva = issue(0, A);
+    for (int s = 0; s < nsteps; s += 2) {
+      const int nvb = issue(s + 1, B);
+      __builtin_amdgcn_sched_barrier(0);
+      if (nva > 0) consume(A, nva);
+      nva = issue(s + 2, A);
+      __builtin_amdgcn_sched_barrier(0);
+      if (nvb > 0) consume(B, nvb);
     }
   }
 
@@ -258,48 +298,62 @@ paged_decode_fast(const DecodeArgs a) {
 }
 
 // Combines the partition partials of every (b, h) whose context spans more
-// than one partition.
-template <typename T, int LPH>
+// than one partition. One wavefront per (b, h): lanes take partitions for the
+// max and the weights, then lanes take head_dim elements and sweep the
+// partitions with the weight of each broadcast from its lane.
+constexpr int kMergeMaxD = 256;
+
+template <typename T>
 __global__ void __launch_bounds__(64)
 paged_decode_merge(const DecodeArgs a) {
-  constexpr int HPW = 64 / LPH;
+  constexpr int NJ = kMergeMaxD / 64;
   const int lane = (int)threadIdx.x;
-  const int sub = lane % LPH;
-  const int row = lane / LPH;
+  const int h = (int)blockIdx.x;
   const int b = (int)blockIdx.y;
-  const int h = (int)blockIdx.x * HPW + row;
   const int D = a.D;
-  if (h >= a.H || sub * 8 >= D) return;
   const int ctx = clamp_ctx<T>(a, b);
   const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
   if (nparts <= 1) return;
-
   const size_t base = ((size_t)b * a.H + h) * a.max_parts;
-  float M = -INFINITY;
-  for (int p = 0; p < nparts; ++p) M = fmaxf(M, a.ws_ml[base + p].x);
-  float L = 0.f;
-  float acc[8];
+
+  float mloc = -INFINITY;
+  for (int p = lane; p < nparts; p += 64) mloc = fmaxf(mloc, a.ws_ml[base + p].x);
+  const float M = wave_max(mloc);
+
+  float acc[NJ];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  for (int j = 0; j < NJ; ++j) acc[j] = 0.f;
+  float lsum = 0.f;
   if (M != -INFINITY) {
-    for (int p = 0; p < nparts; ++p) {
-      const float2 ml = a.ws_ml[base + p];
-      const float w = fast_exp2(ml.x - M);
-      L = fmaf(w, ml.y, L);
-      const float* wa = a.ws_acc + (base + p) * D;
-      const float4 x0 = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 0));
-      const float4 x1 = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 4));
-      acc[0] = fmaf(w, x0.x, acc[0]);
-      acc[1] = fmaf(w, x0.y, acc[1]);
-      acc[2] = fmaf(w, x0.z, acc[2]);
-      acc[3] = fmaf(w, x0.w, acc[3]);
-      acc[4] = fmaf(w, x1.x, acc[4]);
-      acc[5] = fmaf(w, x1.y, acc[5]);
-      acc[6] = fmaf(w, x1.z, acc[6]);
-      acc[7] = fmaf(w, x1.w, acc[7]);
+    for (int p0 = 0; p0 < nparts; p0 += 64) {
+      // weight of partition p0 + lane
+      float w = 0.f;
+      if (p0 + lane < nparts) {
+        const float2 ml = a.ws_ml[base + p0 + lane];
+        w = fast_exp2(ml.x - M);
+        lsum = fmaf(w, ml.y, lsum);
+      }
+      const int n = min(64, nparts - p0);
+      const float* wa = a.ws_acc + (base + p0) * D;
+#pragma unroll 4
+      for (int i = 0; i < n; ++i) {
+        const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int d = lane + 64 * j;
+          if (d < D) acc[j] = fmaf(wi, wa[(size_t)i * D + d], acc[j]);
+        }
+      }
     }
   }
-  store_out<T>(a, b, h, sub, acc, L > 0.f ? 1.f / L : 0.f);
+  const float L = wave_sum(lsum);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) Elem<T>::store(orow + (int64_t)d * a.o_sd, acc[j] * inv);
+  }
 }
 
 // ----------------------------------------------------------- generic kernel
@@ -341,7 +395,7 @@ paged_decode_generic(const DecodeArgs a) {
         const int d = lane + 64 * j;
         if (d < D) part = fmaf(q[j], Elem<T>::load(kt + (int64_t)d * a.k_sd), part);
       }
-      const float s = wave_sum(part) * a.scale_log2;
+      const float s = __fmul_rn(wave_sum(part), a.scale_log2);
       const float mn = fmaxf(m, s);
       const float alpha = fast_exp2(m - mn);
       const float p = fast_exp2(s - mn);
@@ -383,17 +437,19 @@ static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_
                         : reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, false>);
   hipError_t e = launch(fn, grid, dim3(64), a, stream);
   if (e != hipSuccess || a.max_parts <= 1) return e;
-  const dim3 mgrid((unsigned)((a.H + HPW - 1) / HPW), (unsigned)a.B);
-  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH>), mgrid, dim3(64), a,
-                stream);
+  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T>),
+                dim3((unsigned)a.H, (unsigned)a.B), dim3(64), a, stream);
 }
 
 template <typename T, int LPH>
 static hipError_t launch_fast_lph(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
   if constexpr (sizeof(T) == 2) {
     if (p.tokens_per_step == 16) return launch_fast_lph_tok<T, LPH, 16>(a, p.full_lanes, stream);
+    if (p.tokens_per_step == 8) return launch_fast_lph_tok<T, LPH, 8>(a, p.full_lanes, stream);
+  } else {
+    if (p.tokens_per_step == 8) return launch_fast_lph_tok<T, LPH, 8>(a, p.full_lanes, stream);
+    if (p.tokens_per_step == 4) return launch_fast_lph_tok<T, LPH, 4>(a, p.full_lanes, stream);
   }
-  if (p.tokens_per_step == 8) return launch_fast_lph_tok<T, LPH, 8>(a, p.full_lanes, stream);
   return hipErrorInvalidValue;
 }
 

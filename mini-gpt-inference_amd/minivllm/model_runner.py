@@ -1,0 +1,111 @@
+"""Runtime state -> device tensors (minivllm/model_runner.py:10-304).
+
+``decode_batch`` reserves one KV slot per sequence (possibly allocating a
+block), builds DecodeBatchMetadata, runs one batched decode step, commits
+``length += 1`` and returns ``(logits[:, -1, :], greedy next tokens)``.
+
+The metadata of a step (input ids, positions, context lengths, slot
+mapping and the -1 padded block tables) is packed into one int64 host
+buffer and moved with a single host-to-device copy; every field is a
+contiguous view of that device buffer. The reference issues about B + 5
+separate copies (one per block-table row, minivllm/model_runner.py:191-201).
+"""
+from __future__ import annotations
+
+import torch
+
+from .block_manager import BlockManager
+from .decode_batch_metadata import DecodeBatchMetadata
+from .kv_block_pool import KVBlockPool
+from .kv_runtime import KVRuntimeContext, PrefillChunkContext, PrefillRuntimeContext
+from .model import MiniGPT
+from .sequence import SequenceState
+
+
+class ModelRunner:
+    def __init__(self, model: MiniGPT, kv_pool: KVBlockPool, block_manager: BlockManager):
+        self.model = model
+        self.kv_pool = kv_pool
+        self.block_manager = block_manager
+
+    @property
+    def device(self) -> torch.device:
+        return next(self.model.parameters()).device
+
+    # ------------------------------------------------------------- prefill
+
+    def prefill(self, seq: SequenceState) -> int:
+        """Whole-prompt prefill; returns the greedy first token."""
+        T = len(seq.prompt_tokens)
+        start = seq.length
+        input_ids = torch.tensor([seq.prompt_tokens], device=self.device, dtype=torch.long)
+        slots = self.block_manager.reserve_slots(seq, T)
+        contexts = [PrefillRuntimeContext(seq_state=seq, kv_pool=self.kv_pool, layer_idx=i,
+                                          start_pos=start, context_length=start + T, slot_mapping=slots)
+                    for i in range(self.model.n_layer)]
+        logits = self.model.prefill(input_ids, contexts)
+        seq.length += T
+        return int(torch.argmax(logits[:, -1], dim=-1).item())
+
+    def prefill_chunk(self, seq: SequenceState, start_pos: int, num_tokens: int) -> torch.Tensor:
+        assert start_pos == seq.prompt_pos
+        assert start_pos == seq.length
+        # A resumed request recomputes its cached prefix (prompt +
+        # generated[:-1]); the pending last token stays for decode.
+        tokens = seq.prefill_input_tokens[start_pos:start_pos + num_tokens]
+        assert len(tokens) == num_tokens, "prefill chunk exceeds input prefix"
+        input_ids = torch.tensor([tokens], device=self.device, dtype=torch.long)
+        slots = self.block_manager.reserve_slots(seq=seq, num_tokens=num_tokens)
+        contexts = [PrefillChunkContext(seq_state=seq, kv_pool=self.kv_pool, layer_idx=i,
+                                        start_pos=start_pos, num_tokens=num_tokens, slot_mapping=slots)
+                    for i in range(self.model.n_layer)]
+        logits = self.model.prefill_chunk(input_ids=input_ids, contexts=contexts)
+        seq.length += num_tokens
+        return logits
+
+    # -------------------------------------------------------------- decode
+
+    def _prepare_decode_batch(self, sequences: list[SequenceState]):
+        B = len(sequences)
+        assert B > 0
+        slots = [self.block_manager.reserve_append_slot(seq)[2] for seq in sequences]
+        M = max(len(seq.block_table) for seq in sequences)
+        # [input_ids | positions | context_lengths | slot_mapping | block_tables]
+        host = torch.full((4 * B + B * M,), -1, dtype=torch.long)
+        host[0:B] = torch.tensor([seq.last_token for seq in sequences], dtype=torch.long)
+        host[B:2 * B] = torch.tensor([seq.length for seq in sequences], dtype=torch.long)
+        host[2 * B:3 * B] = host[B:2 * B] + 1
+        host[3 * B:4 * B] = torch.tensor(slots, dtype=torch.long)
+        tables = host[4 * B:].view(B, M)
+        for b, seq in enumerate(sequences):
+            tables[b, :len(seq.block_table)] = torch.tensor(seq.block_table, dtype=torch.long)
+        dev = host.to(self.device)
+        metadata = DecodeBatchMetadata(
+            positions=dev[B:2 * B],
+            context_lengths=dev[2 * B:3 * B],
+            block_tables=dev[4 * B:].view(B, M),
+            slot_mapping=dev[3 * B:4 * B],
+        )
+        return dev[0:B].view(B, 1), metadata
+
+    def decode_one(self, seq: SequenceState) -> int:
+        """Serial one-sequence decode; returns the greedy next token."""
+        block, offset, slot = self.block_manager.reserve_append_slot(seq)
+        contexts = [KVRuntimeContext(seq_state=seq, block_manager=self.block_manager, kv_pool=self.kv_pool,
+                                     layer_idx=i, logical_pos=seq.length, context_length=seq.length + 1,
+                                     physical_block=block, block_offset=offset, physical_slot=slot)
+                    for i in range(self.model.n_layer)]
+        input_ids = torch.tensor([[seq.last_token]], device=self.device, dtype=torch.long)
+        logits = self.model.decode(input_ids=input_ids, contexts=contexts)
+        seq.length += 1
+        return int(torch.argmax(logits[:, -1], dim=-1).item())
+
+    def decode_batch(self, sequences: list[SequenceState]):
+        if not sequences:
+            return []
+        input_ids, metadata = self._prepare_decode_batch(sequences=sequences)
+        logits = self.model.decode_batch(input_ids=input_ids, metadata=metadata, kv_pool=self.kv_pool)
+        for seq in sequences:
+            seq.length += 1
+        last = logits[:, -1, :]
+        return last, torch.argmax(last, dim=-1).tolist()

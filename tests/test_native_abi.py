@@ -34,18 +34,20 @@ def test_library_exports_every_declared_symbol():
 
 def test_split_tokens_and_workspace_sizes():
     lib = _native.lib()
-    # decode microbench shape: M = 256 columns of S = 16 -> 16 partitions of 256
-    assert lib.mgi_paged_decode_split_tokens(64, 32, 128, 16, 256, 0) == 256
-    n = 64 * 32 * 16
+    # decode microbench shape: M = 256 columns of S = 16 -> 8 partitions of 512
+    assert lib.mgi_paged_decode_split_tokens(64, 32, 128, 16, 256, 0) == 512
+    n = 64 * 32 * 8
     acc = n * 128 * 4
     assert lib.mgi_paged_decode_workspace_bytes(64, 32, 128, 16, 256, 0) == ((acc + 255) // 256) * 256 + n * 8
     # a table that fits one partition needs no workspace
     assert lib.mgi_paged_decode_workspace_bytes(4, 8, 32, 16, 4, 0) == 0
-    for S, M, req in [(16, 8192, 0), (8, 100, 0), (12, 77, 100), (16, 256, 1), (16, 256, 5000)]:
+    for S, M, req in [(16, 8192, 0), (8, 100, 0), (12, 77, 100), (16, 256, 1), (16, 256, 5000),
+                      (1, 10**6, 0), (16, 3, 0)]:
         P = lib.mgi_paged_decode_split_tokens(1, 1, 128, S, M, req)
-        assert P % S == 0 or P == M * S
-        assert 0 < P <= M * S
+        assert P % S == 0                     # partitions start on block boundaries
+        assert 0 < P <= min(M * S, 128 * S)   # at most 128 blocks per partition
         assert (M * S + P - 1) // P <= 65535
+    assert lib.mgi_paged_decode_split_tokens(1, 1, 128, 16, 256, 5000) == 2048
 
 
 def _i64(*xs):
