@@ -242,13 +242,15 @@ paged_decode_fast(const DecodeArgs a) {
 
   // Folds one step into the online softmax (scores in the log2 domain).
   auto consume = [&](const Step<T, TOK>& st, int nvalid) {
+    // No implicit FMA contraction: a score and the running max derived from
+    // it must be the same rounded value, so the largest score's weight is
+    // exactly 2^0 = 1 (explicit fmaf / dot2 calls are unaffected).
+#pragma clang fp contract(off)
     float s[TOK];
     float mb = -INFINITY;
 #pragma unroll
     for (int t = 0; t < TOK; ++t) {
-      // Rounded multiply (never fused into the exponent's subtraction), so the
-      // largest score minus the running max is exactly 0 and its weight is 1.
-      const float d = __fmul_rn(group_sum<LPH>(q.dot(st.k[t])), a.scale_log2);
+      const float d = group_sum<LPH>(q.dot(st.k[t])) * a.scale_log2;
       s[t] = t < nvalid ? d : -INFINITY;
       mb = fmaxf(mb, s[t]);
     }
@@ -385,6 +387,7 @@ paged_decode_generic(const DecodeArgs a) {
   int blk = 0, off = 0;
   int64_t phys = 0;
   for (int t = 0; t < ctx; ++t) {
+#pragma clang fp contract(off)
     if (off == 0) phys = load_index(a.bt, a.bt_i64, bt_row + (int64_t)blk * a.bt_sm);
     if (phys >= 0 && phys < a.N) {
       const T* kt = kh + phys * a.k_sn + (int64_t)off * a.k_ss;
@@ -395,7 +398,7 @@ paged_decode_generic(const DecodeArgs a) {
         const int d = lane + 64 * j;
         if (d < D) part = fmaf(q[j], Elem<T>::load(kt + (int64_t)d * a.k_sd), part);
       }
-      const float s = __fmul_rn(wave_sum(part), a.scale_log2);
+      const float s = wave_sum(part) * a.scale_log2;
       const float mn = fmaxf(m, s);
       const float alpha = fast_exp2(m - mn);
       const float p = fast_exp2(s - mn);
