@@ -41,11 +41,37 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 // live in two VGPRs of the wavefront).
 constexpr int64_t kMaxBlocksPerPart = 128;
 
-// Partition size in tokens: a multiple of S, at most kMaxBlocksPerPart
-// blocks, and the whole table when that fits in one partition.
-int64_t split_tokens_for(int64_t S, int64_t M, int64_t requested) {
+// Compute units of the current device (256 on MI355X; 256 when no device is
+// visible, e.g. for host-only size queries).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    cached[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                   n > 0) ? n : 256;
+  }
+  return cached[dev];
+}
+
+// Partition size in tokens: a multiple of S, at most kMaxBlocksPerPart blocks
+// and at most the table's M*S. Automatic choice: the smallest power of two
+// >= 256 for which the grid, sized for contexts filling the table, holds
+// about four wavefronts per SIMD of the chip (4 heads per wavefront at
+// head_dim 128). Measured on MI355X: ragged 512-4096 contexts at B=64 and
+// 32k-128k contexts at B=8 both sit within ~1% of their best split there.
+int64_t split_tokens_for(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
+                         int64_t requested) {
   const int64_t max_ctx = M * S;
-  int64_t P = requested > 0 ? requested : 512;
+  int64_t P = requested;
+  if (P <= 0) {
+    const int64_t lph = D <= 32 ? 4 : D <= 64 ? 8 : D <= 128 ? 16 : 32;
+    const int64_t waves_per_part = B * ((H + 64 / lph - 1) / (64 / lph));
+    const int64_t target = 4 * 4 * (int64_t)device_cus();  // 4 SIMDs per CU
+    P = 256;
+    while (P < max_ctx && waves_per_part * ((max_ctx + P - 1) / P) > target) P *= 2;
+  }
   P = std::min(round_up(P, S), kMaxBlocksPerPart * S);
   return std::min(P, max_ctx);
 }
@@ -67,10 +93,11 @@ WorkspaceLayout workspace_layout(int64_t B, int64_t H, int64_t D, int64_t S, int
   return w;
 }
 
-// Tokens loaded per pipeline stage of the fast kernel: 8 for bf16 and 4 for
-// f32 (16 KiB of K+V per stage and wavefront at head_dim 128), or the largest
-// of those S allows. MINIVLLM_HIP_TOKENS_PER_STEP (4, 8, or 16 for bf16)
-// overrides the choice when S allows it (tuning).
+// Tokens loaded per pipeline stage of the fast kernel: 16 for bf16 and 8 for
+// f32 (32 KiB of K+V per stage and wavefront at head_dim 128; two stages in
+// flight), or the largest S allows. Measured on MI355X this beats smaller
+// stages at higher occupancy. MINIVLLM_HIP_TOKENS_PER_STEP (4, 8, or 16 for
+// bf16) overrides the choice when S allows it (tuning).
 int tokens_per_step_override() {
   static const int v = [] {
     const char* e = std::getenv("MINIVLLM_HIP_TOKENS_PER_STEP");
@@ -95,17 +122,14 @@ int mgi_abi_version(void) { return 100; }
 
 int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                       int64_t split_tokens) {
-  (void)B;
-  (void)H;
-  (void)D;
-  if (S <= 0 || M <= 0) return 0;
-  return split_tokens_for(S, M, split_tokens);
+  if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || M <= 0) return 0;
+  return split_tokens_for(B, H, D, S, M, split_tokens);
 }
 
 size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                         int64_t split_tokens) {
   if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || M <= 0) return 0;
-  const int64_t P = split_tokens_for(S, M, split_tokens);
+  const int64_t P = split_tokens_for(B, H, D, S, M, split_tokens);
   return workspace_layout(B, H, D, S, M, P).total;
 }
 
@@ -144,7 +168,7 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   const char* kbase = static_cast<const char*>(k_pool) + layer_idx * k_pool_strides[0] * eb;
   const char* vbase = static_cast<const char*>(v_pool) + layer_idx * v_pool_strides[0] * eb;
 
-  const int64_t P = split_tokens_for(S, M, split_tokens);
+  const int64_t P = split_tokens_for(B, H, D, S, M, split_tokens);
   const WorkspaceLayout ws = workspace_layout(B, H, D, S, M, P);
 
   // Path selection: the fast kernel needs unit d-stride, 16-byte aligned head
@@ -161,7 +185,7 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
       std::max(k_pool_strides[2], v_pool_strides[2]) * eb * S < (int64_t(1) << 31)) {
     int tok = 0;
     const int want = tokens_per_step_override();
-    const int def = dtype == MGI_BF16 ? 8 : 4;
+    const int def = dtype == MGI_BF16 ? 16 : 8;
     for (int t : {want, def, 8, 4}) {
       if (t > 0 && (t == 4 || t == 8 || (t == 16 && dtype == MGI_BF16)) && S % t == 0) {
         tok = t;
