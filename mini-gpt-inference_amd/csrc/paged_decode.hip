@@ -300,62 +300,70 @@ paged_decode_fast(const DecodeArgs a) {
 }
 
 // Combines the partition partials of every (b, h) whose context spans more
-// than one partition. One wavefront per (b, h): lanes take partitions for the
-// max and the weights, then lanes take head_dim elements and sweep the
-// partitions with the weight of each broadcast from its lane.
-constexpr int kMergeMaxD = 256;
-
-template <typename T>
+// than one partition. One wavefront per (sequence, HPW heads), the fast
+// kernel's head grouping: in each head row, lane j loads the (max, sum) of
+// partition p0 + j while every lane loads its 8 elements of all CH partial
+// outputs of the chunk, so a chunk costs one round trip; chunks fold online:
+//   M' = max(M, max_j m_j), L' = L 2^(M-M') + sum_j l_j 2^(m_j-M'),
+//   O' = O 2^(M-M') + sum_j O_j 2^(m_j-M').
+template <typename T, int LPH>
 __global__ void __launch_bounds__(64)
 paged_decode_merge(const DecodeArgs a) {
-  constexpr int NJ = kMergeMaxD / 64;
+  constexpr int HPW = 64 / LPH;
+  constexpr int CH = LPH < 16 ? LPH : 16;  // partitions per chunk
   const int lane = (int)threadIdx.x;
-  const int h = (int)blockIdx.x;
+  const int sub = lane % LPH;
+  const int row = lane / LPH;
   const int b = (int)blockIdx.y;
+  const int h = (int)blockIdx.x * HPW + row;
   const int D = a.D;
+  const bool head_ok = h < a.H;
+  const bool lane_ok = head_ok && sub * 8 < D;
   const int ctx = clamp_ctx<T>(a, b);
   const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
-  if (nparts <= 1) return;
-  const size_t base = ((size_t)b * a.H + h) * a.max_parts;
+  if (nparts <= 1) return;  // uniform over the wave
+  const size_t base = ((size_t)b * a.H + (head_ok ? h : 0)) * a.max_parts;
 
-  float mloc = -INFINITY;
-  for (int p = lane; p < nparts; p += 64) mloc = fmaxf(mloc, a.ws_ml[base + p].x);
-  const float M = wave_max(mloc);
-
-  float acc[NJ];
+  float M = -INFINITY, L = 0.f;
+  float acc[8];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) acc[j] = 0.f;
-  float lsum = 0.f;
-  if (M != -INFINITY) {
-    for (int p0 = 0; p0 < nparts; p0 += 64) {
-      // weight of partition p0 + lane
-      float w = 0.f;
-      if (p0 + lane < nparts) {
-        const float2 ml = a.ws_ml[base + p0 + lane];
-        w = fast_exp2(ml.x - M);
-        lsum = fmaf(w, ml.y, lsum);
-      }
-      const int n = min(64, nparts - p0);
-      const float* wa = a.ws_acc + (base + p0) * D;
-#pragma unroll 4
-      for (int i = 0; i < n; ++i) {
-        const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  for (int p0 = 0; p0 < nparts; p0 += CH) {
+    float2 ml = make_float2(-INFINITY, 0.f);
+    if (head_ok && sub < CH && p0 + sub < nparts) ml = a.ws_ml[base + p0 + sub];
+    float4 x0[CH], x1[CH];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int d = lane + 64 * j;
-          if (d < D) acc[j] = fmaf(wi, wa[(size_t)i * D + d], acc[j]);
-        }
+    for (int j = 0; j < CH; ++j) {
+      if (lane_ok && p0 + j < nparts) {
+        const float* wa = a.ws_acc + (base + p0 + j) * D;
+        x0[j] = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 0));
+        x1[j] = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 4));
+      } else {
+        x0[j] = x1[j] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
-  }
-  const float L = wave_sum(lsum);
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+    const float Mn = fmaxf(M, group_reduce<LPH, MaxOp>(ml.x));
+    const float alpha = (M == Mn) ? 1.f : fast_exp2(M - Mn);
+    const float w = (ml.x == -INFINITY) ? 0.f : fast_exp2(ml.x - Mn);
+    L = L * alpha + group_sum<LPH>(w * ml.y);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int d = lane + 64 * j;
-    if (d < D) Elem<T>::store(orow + (int64_t)d * a.o_sd, acc[j] * inv);
+    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const float wj = __shfl(w, row * LPH + j, 64);  // weight of partition p0 + j
+      acc[0] = fmaf(wj, x0[j].x, acc[0]);
+      acc[1] = fmaf(wj, x0[j].y, acc[1]);
+      acc[2] = fmaf(wj, x0[j].z, acc[2]);
+      acc[3] = fmaf(wj, x0[j].w, acc[3]);
+      acc[4] = fmaf(wj, x1[j].x, acc[4]);
+      acc[5] = fmaf(wj, x1[j].y, acc[5]);
+      acc[6] = fmaf(wj, x1[j].z, acc[6]);
+      acc[7] = fmaf(wj, x1[j].w, acc[7]);
+    }
+    M = Mn;
   }
+  if (!lane_ok) return;
+  store_out<T>(a, b, h, sub, acc, L > 0.f ? 1.f / L : 0.f);
 }
 
 // ----------------------------------------------------------- generic kernel
@@ -440,8 +448,8 @@ static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_
                         : reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, false>);
   hipError_t e = launch(fn, grid, dim3(64), a, stream);
   if (e != hipSuccess || a.max_parts <= 1) return e;
-  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T>),
-                dim3((unsigned)a.H, (unsigned)a.B), dim3(64), a, stream);
+  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH>),
+                dim3((unsigned)((a.H + HPW - 1) / HPW), (unsigned)a.B), dim3(64), a, stream);
 }
 
 template <typename T, int LPH>
