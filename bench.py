@@ -22,6 +22,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -139,6 +140,22 @@ def cpu_baseline(w):
             "cpu": _cpu_model()}
 
 
+def profiled_traffic(workload: str, split: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy kernel of
+    known size), when profiles/ holds one for this workload and split."""
+    for md in sorted((ROOT / "profiles").glob("*.md")):
+        for block in re.findall(r"```json\n(.*?)```", md.read_text(), flags=re.S):
+            try:
+                d = json.loads(block)
+            except json.JSONDecodeError:
+                continue
+            if d.get("workload") == workload and d.get("split_tokens") == split:
+                kib = d["fetch_kib_per_dispatch"] * d["fetch_scale"] + d["write_kib_per_dispatch"] * d["write_scale"]
+                return int(kib * 1024), md.name
+    return None, None
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -212,6 +229,8 @@ def main() -> None:
             cpu = cpu_baseline(w)
             log(f"cpu: {cpu}")
 
+    workload_tag = f"decode_microbench_{args.dtype}_B{B}_H{H}_D{D}_ctx512-4096"
+    traffic, traffic_src = profiled_traffic(workload_tag, split)
     result = {
         "metric": METRIC,
         "value": main_line["gbps"],
@@ -231,9 +250,10 @@ def main() -> None:
         "pct_of_peak": main_line["pct_of_peak"],
         "decode_seq_per_s_per_layer": main_line["seq_per_s_per_layer"],
         "roofline": {"bound": "hbm", "achieved": main_line["gbps"], "peak": PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(main_line["gbps"] / PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(main_line["gbps"] / PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "alg_bytes_per_launch": main_line["alg_bytes"],
-                     "kernel": "paged_decode_fast (+ partition merge) per call"},
+                     "kernel": "paged_decode_fast + paged_decode_merge (one mgi_paged_decode call)"},
         "cpu_baseline": cpu,
         "extra": extras,
     }

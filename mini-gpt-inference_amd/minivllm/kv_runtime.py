@@ -3,6 +3,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import torch
+
 from .block_manager import BlockManager
 from .kv_block_pool import KVBlockPool
 from .sequence import SequenceState
@@ -35,10 +37,14 @@ class PrefillRuntimeContext:
 
 @dataclass
 class PrefillChunkContext:
-    """One prefill chunk [start_pos, start_pos + num_tokens) of one layer."""
+    """One prefill chunk [start_pos, start_pos + num_tokens) of one layer.
+
+    slot_mapping is a list of physical slots, or the same slots as an int64
+    tensor on the pool's device (the runner moves them once per chunk).
+    """
     seq_state: SequenceState
     kv_pool: KVBlockPool
     layer_idx: int
     start_pos: int
     num_tokens: int
-    slot_mapping: list[int]
+    slot_mapping: list[int] | torch.Tensor

@@ -56,6 +56,9 @@ class ModelRunner:
         assert len(tokens) == num_tokens, "prefill chunk exceeds input prefix"
         input_ids = torch.tensor([tokens], device=self.device, dtype=torch.long)
         slots = self.block_manager.reserve_slots(seq=seq, num_tokens=num_tokens)
+        if self.kv_pool.k.is_cuda:
+            # One host-to-device copy of the chunk's slots, shared by every layer.
+            slots = torch.tensor(slots, dtype=torch.long, device=self.kv_pool.k.device)
         contexts = [PrefillChunkContext(seq_state=seq, kv_pool=self.kv_pool, layer_idx=i,
                                         start_pos=start_pos, num_tokens=num_tokens, slot_mapping=slots)
                     for i in range(self.model.n_layer)]
