@@ -46,6 +46,11 @@ def parse_args():
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--no-extras", action="store_true", help="skip the other workload shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--e2e", action="store_true",
+                    help="also run the full runtime under recompute preemption (dim 2048, 12 layers, "
+                         "vocab 32000, bf16, 256 requests, 128 output tokens) with the HIP backend and "
+                         "report decode tokens/s")
+    ap.add_argument("--e2e-requests", type=int, default=256)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run a device-to-device copy of this many MiB (3 times) so rocprof "
                          "counters can be scaled by a kernel of known traffic")
@@ -117,6 +122,31 @@ def copy_line(mib: int, dev, reps: int = 3):
     dst = torch.empty_like(src)
     ms = time_steps(lambda: dst.copy_(src), reps, 1)
     return {"mib": mib, "ms": round(ms, 4), "gbps_read_plus_write": round(2 * src.numel() / (ms * 1e-3) / 1e9, 1)}
+
+
+def e2e_line(n_requests: int, dev):
+    """The full runtime under recompute preemption with the HIP decode backend."""
+    import torch
+
+    import _e2e
+
+    spec = _e2e.RuntimeSpec(n_requests=n_requests)
+    prompts = _e2e.make_prompts(spec)
+    model = _e2e.make_model(spec, dev, torch.bfloat16)
+    model.set_decode_attention_backend("hip")
+    # warm-up: a few requests through prefill + decode
+    warm = _e2e.RuntimeSpec(n_requests=4, output_len=4, seed=99)
+    rt, seqs = _e2e.make_runtime(warm, model, _e2e.make_prompts(warm), dev, torch.bfloat16)
+    _e2e.run_to_completion(rt, seqs)
+    del rt, seqs
+    rt, seqs = _e2e.make_runtime(spec, model, prompts, dev, torch.bfloat16)
+    stats = _e2e.run_to_completion(rt, seqs)
+    stats.update({"requests": n_requests, "pool_blocks": _e2e.pool_blocks(spec, prompts),
+                  "sum_prompt_tokens": sum(len(p) for p in prompts),
+                  "model": "MiniGPT dim 2048, 16 heads, 12 layers, vocab 32000, bf16, random init (seed 0)",
+                  "schedule": "max_running 256, token budget 2048, recompute preemption, prefill sdpa_v2",
+                  "decode_backend": "hip"})
+    return stats
 
 
 def cpu_baseline(w):
@@ -217,6 +247,12 @@ def main() -> None:
             log(f"extra append: {extras['kv_append_bf16_B256']}")
             extras["d2d_copy_4GiB"] = copy_line(4096, dev, reps=5)
             log(f"extra copy: {extras['d2d_copy_4GiB']}")
+            torch.cuda.empty_cache()
+
+        if args.e2e:
+            log(f"end-to-end runtime, {args.e2e_requests} requests")
+            extras["e2e_runtime_bf16_preemption"] = e2e_line(args.e2e_requests, dev)
+            log(f"e2e: {extras['e2e_runtime_bf16_preemption']}")
             torch.cuda.empty_cache()
 
         if args.calibrate_copy_mib:
