@@ -140,7 +140,14 @@ def e2e_line(n_requests: int, dev):
     _e2e.run_to_completion(rt, seqs)
     del rt, seqs
     rt, seqs = _e2e.make_runtime(spec, model, prompts, dev, torch.bfloat16)
-    stats = _e2e.run_to_completion(rt, seqs)
+
+    def progress(r):
+        if r.iteration % 25 == 0:
+            s = r.metrics_summary()
+            log(f"e2e step {r.iteration}: output {s['output_tokens']} prefill {s['prefill_tokens']} "
+                f"preemptions {s['preemptions']}")
+
+    stats = _e2e.run_to_completion(rt, seqs, on_step=progress)
     stats.update({"requests": n_requests, "pool_blocks": _e2e.pool_blocks(spec, prompts),
                   "sum_prompt_tokens": sum(len(p) for p in prompts),
                   "model": "MiniGPT dim 2048, 16 heads, 12 layers, vocab 32000, bf16, random init (seed 0)",
