@@ -156,6 +156,62 @@ def e2e_line(n_requests: int, dev):
     return stats
 
 
+def attention_speedup_grid(dev):
+    """HIP decode vs the PyTorch online_v1 backend on the same GPU, over the
+    default grid of the reference's fused-decode A/B script
+    (experiments/gpu_day6_fused_decode_ab.py:231-242): batches 1,2,4;
+    contexts 32,128,256; 8 heads; head_dim 32; block 16; fp32. The reference
+    publishes 12.18x-81.68x for its Triton kernel (RTX 5090)."""
+    import torch
+
+    import _fixtures as fx
+    from minivllm import hip_paged_decode as hpd
+    from minivllm.paged_attention_batch import paged_attention_batch_online_v1
+
+    rows = []
+    for B in (1, 2, 4):
+        for ctx in (32, 128, 256):
+            q, pool, tables, lens, layer = fx.build_case(B, ctx, 8, 32, 16, "mixed")
+            dpool = fx.pool_to_device(pool, dev)
+            qd, td, ld = q.to(dev), tables.to(dev), lens.to(dev)
+            ref_ms = time_steps(lambda: paged_attention_batch_online_v1(qd, dpool, td, ld, layer), 20, 3)
+            hip_ms = time_steps(lambda: hpd.paged_attention_batch_hip(qd, dpool, td, ld, layer), 50, 5)
+            rows.append({"batch": B, "ctx": ctx, "online_v1_ms": round(ref_ms, 4), "hip_ms": round(hip_ms, 4),
+                         "speedup": round(ref_ms / hip_ms, 1)})
+    sp = [r["speedup"] for r in rows]
+    return {"min_speedup": min(sp), "max_speedup": max(sp), "grid": rows}
+
+
+def e2e_c1_speedup(dev):
+    """Mini-GPT end to end (dim 256, 8 heads, 4 layers, vocab 256, fp32; prompts
+    128/256 x batch 1/4; budget 64; 8 greedy tokens): wall time of the whole
+    runtime with the HIP decode backend vs the PyTorch reference backend on the
+    same GPU, and the greedy tokens of both against the reference's golden
+    streams. The reference publishes 3.80x-6.34x for its Triton backend."""
+    import time
+
+    import torch
+
+    import _e2e
+
+    rows = []
+    for case in _e2e.GOLDEN_C1["cases"]:
+        out = {}
+        for backend in ("reference", "hip"):
+            _e2e.run_c1(case, "cuda", backend)          # warm-up
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            tokens, _ = _e2e.run_c1(case, "cuda", backend)
+            torch.cuda.synchronize()
+            out[backend] = (time.perf_counter() - t0, tokens == case["outputs"])
+        rows.append({"batch": case["batch"], "prompt_len": case["prompt_len"],
+                     "reference_s": round(out["reference"][0], 4), "hip_s": round(out["hip"][0], 4),
+                     "speedup": round(out["reference"][0] / out["hip"][0], 2),
+                     "tokens_match_golden": out["reference"][1] and out["hip"][1]})
+    sp = [r["speedup"] for r in rows]
+    return {"min_speedup": min(sp), "max_speedup": max(sp), "cases": rows}
+
+
 def cpu_baseline(w):
     from oracle import c_oracle
 
@@ -254,6 +310,12 @@ def main() -> None:
             log(f"extra append: {extras['kv_append_bf16_B256']}")
             extras["d2d_copy_4GiB"] = copy_line(4096, dev, reps=5)
             log(f"extra copy: {extras['d2d_copy_4GiB']}")
+            torch.cuda.empty_cache()
+            extras["attention_speedup_vs_online_v1"] = attention_speedup_grid(dev)
+            log(f"extra attention speedup: {extras['attention_speedup_vs_online_v1']['min_speedup']}x-"
+                f"{extras['attention_speedup_vs_online_v1']['max_speedup']}x")
+            extras["e2e_small_model_speedup"] = e2e_c1_speedup(dev)
+            log(f"extra e2e speedup: {extras['e2e_small_model_speedup']}")
             torch.cuda.empty_cache()
 
         if args.e2e:

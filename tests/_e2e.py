@@ -1,5 +1,11 @@
 """End-to-end runtime workloads built on the minivllm API.
 
+Mini-GPT configuration with golden greedy tokens (``run_c1``): dim 256,
+8 heads, 4 layers, vocab 256, fp32, seed 0; paged KV block 16; prompts of
+128/256 tokens, batch 1/4; chunked prefill with token budget 64; 8 greedy
+tokens. Inputs and the reference runtime's outputs are in
+golden/c1_greedy_tokens.json (written by golden/make_c1_greedy_tokens.py).
+
 Full runtime under recompute preemption (the large end-to-end configuration):
   model     MiniGPT(n_embd=2048, n_head=16, vocab_size=32000,
             block_size=max_prompt + output, n_layer=12), random init after
@@ -15,9 +21,11 @@ Reduced variants (fewer requests / layers / tokens) keep the same recipe.
 """
 from __future__ import annotations
 
+import json
 import math
 import time
 from dataclasses import dataclass
+from pathlib import Path
 
 import numpy as np
 import torch
@@ -116,3 +124,44 @@ def run_to_completion(rt: MiniRuntime, seqs, max_steps: int = 100000, on_step=No
             "output_tok_s": round(summ["output_tokens"] / wall, 1),
             "decode_tok_s_in_decode_phase": round(summ["decode_tokens"] / (decode_ms / 1e3), 1) if decode_ms else None,
             "decode_ms_total": round(decode_ms, 1)}
+
+
+# ------------------------------------------------- golden-token configuration
+
+GOLDEN_C1 = json.loads((Path(__file__).resolve().parent / "golden" / "c1_greedy_tokens.json").read_text())
+
+
+def run_c1(case: dict, device, backend: str):
+    """Runs one golden case; returns (generated tokens per request, runtime)."""
+    cfg = GOLDEN_C1["config"]
+    torch.manual_seed(cfg["seed"])
+    model = MiniGPT(n_embd=cfg["n_embd"], n_head=cfg["n_head"], vocab_size=cfg["vocab_size"],
+                    block_size=cfg["block_size"], dropout=0.0, n_layer=cfg["n_layer"]).eval().to(device)
+    model.set_prefill_fastpath_mode(cfg["prefill_mode"])
+    model.set_decode_attention_backend(backend)
+    B, P, S = case["batch"], case["prompt_len"], cfg["block_size_kv"]
+    blocks = B * math.ceil((P + cfg["output_len"] - 1) / S)
+    assert blocks == case["num_blocks"]
+    manager = BlockManager(num_blocks=blocks, block_size=S)
+    rt = MiniRuntime.__new__(MiniRuntime)
+    rt.block_manager = manager
+    rt.scheduler = Scheduler(manager, max_running=B, max_num_batched_tokens=cfg["token_budget"],
+                             preemption_policy="conservative")
+    pool = KVBlockPool(n_layer=cfg["n_layer"], num_blocks=blocks, block_size=S, n_head=cfg["n_head"],
+                       head_dim=cfg["n_embd"] // cfg["n_head"], device=device)
+    pool.k.fill_(float("nan"))
+    pool.v.fill_(float("nan"))
+    rt.runner = ModelRunner(model, pool, manager)
+    rt.iteration, rt.records = 0, []
+    seqs = [SequenceState(seq_id=f"req_{i:02d}", prompt_tokens=case["prompts"][i],
+                          max_tokens=P + cfg["output_len"]) for i in range(B)]
+    for s in seqs:
+        rt.add_request(s)
+    with torch.inference_mode():
+        for _ in range(1000):
+            if all(s.status == Status.FINISHED for s in seqs):
+                break
+            rt.step()
+            manager.check_invariants([s for s in seqs if s.status != Status.FINISHED])
+    assert all(s.status == Status.FINISHED for s in seqs)
+    return [s.generated_tokens for s in seqs], rt
