@@ -124,8 +124,10 @@ def copy_line(mib: int, dev, reps: int = 3):
     return {"mib": mib, "ms": round(ms, 4), "gbps_read_plus_write": round(2 * src.numel() / (ms * 1e-3) / 1e9, 1)}
 
 
-def e2e_line(n_requests: int, dev):
-    """The full runtime under recompute preemption with the HIP decode backend."""
+def e2e_line(n_requests: int, dev, graphs: bool):
+    """The full runtime under recompute preemption with the HIP decode backend;
+    with `graphs`, decode steps replay HIP graphs captured (before timing) for
+    every batch bucket up to max_running."""
     import torch
 
     import _e2e
@@ -140,6 +142,9 @@ def e2e_line(n_requests: int, dev):
     _e2e.run_to_completion(rt, seqs)
     del rt, seqs
     rt, seqs = _e2e.make_runtime(spec, model, prompts, dev, torch.bfloat16)
+    if graphs:
+        rt.runner.enable_decode_graphs()
+        rt.runner.capture_decode_graphs([b for b in (1, 2, 4, 8, 16, 32, 64, 128, 256) if b <= spec.max_running])
 
     def progress(r):
         if r.iteration % 25 == 0:
@@ -152,7 +157,8 @@ def e2e_line(n_requests: int, dev):
                   "sum_prompt_tokens": sum(len(p) for p in prompts),
                   "model": "MiniGPT dim 2048, 16 heads, 12 layers, vocab 32000, bf16, random init (seed 0)",
                   "schedule": "max_running 256, token budget 2048, recompute preemption, prefill sdpa_v2",
-                  "decode_backend": "hip"})
+                  "decode_backend": "hip", "decode_graphs": graphs,
+                  "tokens": [s.generated_tokens for s in seqs]})
     return stats
 
 
@@ -319,10 +325,16 @@ def main() -> None:
             torch.cuda.empty_cache()
 
         if args.e2e:
-            log(f"end-to-end runtime, {args.e2e_requests} requests")
-            extras["e2e_runtime_bf16_preemption"] = e2e_line(args.e2e_requests, dev)
-            log(f"e2e: {extras['e2e_runtime_bf16_preemption']}")
-            torch.cuda.empty_cache()
+            for graphs in (False, True):
+                key = "e2e_runtime_bf16_preemption" + ("_graphs" if graphs else "")
+                log(f"end-to-end runtime, {args.e2e_requests} requests, decode graphs {graphs}")
+                extras[key] = e2e_line(args.e2e_requests, dev, graphs)
+                torch.cuda.empty_cache()
+            eager, graph = extras["e2e_runtime_bf16_preemption"], extras["e2e_runtime_bf16_preemption_graphs"]
+            same = sum(a == b for a, b in zip(eager.pop("tokens"), graph.pop("tokens")))
+            graph["identical_token_streams_vs_eager"] = f"{same}/{args.e2e_requests}"
+            log(f"e2e: eager {eager}")
+            log(f"e2e: graphs {graph}")
 
         if args.calibrate_copy_mib:
             extras["copy_calibration"] = copy_line(args.calibrate_copy_mib, dev, reps=3)

@@ -1,0 +1,115 @@
+"""Captured decode steps: the whole batched decode step (embeddings, every
+layer's projections, KV append and paged decode attention, MLP, final norm,
+LM head and the greedy argmax) recorded once per batch-size bucket as a HIP
+graph and replayed each step.
+
+A step's metadata (input ids, positions, context lengths, slot mapping and
+block tables) lives in one static int64 device buffer per bucket; a step
+fills it with a single host-to-device copy and replays. The block-table
+width is fixed at the most blocks one sequence can hold, so one graph per
+batch bucket serves every context length. Rows past the real batch are
+padding: slot -1 (the KV append skips them), context length 0 (attention
+writes zeros), token and position 0; their logits are discarded.
+
+Capture needs the HIP decode backend: the PyTorch reference backend reads
+device data on the host while filtering padding slots, which a graph cannot
+record.
+"""
+from __future__ import annotations
+
+import torch
+
+from .decode_batch_metadata import DecodeBatchMetadata
+from .kv_block_pool import KVBlockPool
+
+DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
+
+
+def pack_decode_metadata(tokens, positions, slots, tables, B_pad: int, M: int) -> torch.Tensor:
+    """Host int64 buffer [ids | positions | context_lengths | slots | tables]
+    for B_pad rows (rows past len(tokens) are padding) and table width M."""
+    B = len(tokens)
+    host = torch.full((4 * B_pad + B_pad * M,), -1, dtype=torch.long)
+    host[0:B_pad] = 0
+    host[B_pad:3 * B_pad] = 0
+    host[0:B] = torch.tensor(tokens, dtype=torch.long)
+    host[B_pad:B_pad + B] = torch.tensor(positions, dtype=torch.long)
+    host[2 * B_pad:2 * B_pad + B] = host[B_pad:B_pad + B] + 1
+    host[3 * B_pad:3 * B_pad + B] = torch.tensor(slots, dtype=torch.long)
+    view = host[4 * B_pad:].view(B_pad, M)
+    for b, table in enumerate(tables):
+        if table:
+            view[b, :len(table)] = torch.tensor(table, dtype=torch.long)
+    return host
+
+
+def metadata_views(buf: torch.Tensor, B_pad: int, M: int):
+    """(input_ids [B,1], DecodeBatchMetadata) as views of a packed buffer."""
+    meta = DecodeBatchMetadata(
+        positions=buf[B_pad:2 * B_pad],
+        context_lengths=buf[2 * B_pad:3 * B_pad],
+        block_tables=buf[4 * B_pad:].view(B_pad, M),
+        slot_mapping=buf[3 * B_pad:4 * B_pad],
+    )
+    return buf[0:B_pad].view(B_pad, 1), meta
+
+
+class _Captured:
+    def __init__(self, model, pool: KVBlockPool, B_pad: int, M: int):
+        dev = pool.k.device
+        self.B_pad, self.M = B_pad, M
+        self.buf = pack_decode_metadata([], [], [], [], B_pad, M).to(dev)
+        ids, meta = metadata_views(self.buf, B_pad, M)
+        with torch.inference_mode():
+            side = torch.cuda.Stream(device=dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                for _ in range(2):  # padding rows only: nothing is written to the pool
+                    model.decode_batch(input_ids=ids, metadata=meta, kv_pool=pool)
+            torch.cuda.current_stream(dev).wait_stream(side)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                logits = model.decode_batch(input_ids=ids, metadata=meta, kv_pool=pool)
+                self.logits = logits[:, -1, :]
+                self.tokens = torch.argmax(self.logits, dim=-1)
+
+    def replay(self, host: torch.Tensor, B: int):
+        self.buf.copy_(host)
+        self.graph.replay()
+        return self.logits[:B].clone(), self.tokens[:B].tolist()
+
+
+class DecodeGraphs:
+    """Per-bucket captured decode steps of one (model, pool) pair."""
+
+    def __init__(self, model, pool: KVBlockPool, max_blocks_per_seq: int,
+                 buckets: tuple[int, ...] = DEFAULT_BUCKETS):
+        from .attention import HIP_BACKENDS
+
+        if not pool.k.is_cuda:
+            raise ValueError("decode graphs need the KV pool on a GPU")
+        backends = {blk.attn.decode_attention_backend for blk in model.blocks}
+        if not backends <= set(HIP_BACKENDS):
+            raise ValueError("decode graphs need the hip decode backend")
+        if max_blocks_per_seq < 1:
+            raise ValueError("max_blocks_per_seq must be positive")
+        self.model, self.pool, self.M = model, pool, int(max_blocks_per_seq)
+        self.buckets = tuple(sorted(buckets))
+        self._graphs: dict[int, _Captured] = {}
+
+    def bucket(self, B: int) -> int | None:
+        return next((b for b in self.buckets if b >= B), None)
+
+    def capture(self, B_pad: int) -> None:
+        if B_pad not in self._graphs:
+            self._graphs[B_pad] = _Captured(self.model, self.pool, B_pad, self.M)
+
+    def run(self, tokens, positions, slots, tables):
+        """One decode step for len(tokens) rows; None if no bucket fits."""
+        B = len(tokens)
+        B_pad = self.bucket(B)
+        if B_pad is None or max(len(t) for t in tables) > self.M:
+            return None
+        self.capture(B_pad)
+        host = pack_decode_metadata(tokens, positions, slots, tables, B_pad, self.M)
+        return self._graphs[B_pad].replay(host, B)

@@ -9,13 +9,15 @@ mapping and the -1 padded block tables) is packed into one int64 host
 buffer and moved with a single host-to-device copy; every field is a
 contiguous view of that device buffer. The reference issues about B + 5
 separate copies (one per block-table row, minivllm/model_runner.py:191-201).
+With ``enable_decode_graphs`` the step replays a captured HIP graph instead
+(minivllm.decode_graphs).
 """
 from __future__ import annotations
 
 import torch
 
 from .block_manager import BlockManager
-from .decode_batch_metadata import DecodeBatchMetadata
+from .decode_graphs import DEFAULT_BUCKETS, DecodeGraphs, metadata_views, pack_decode_metadata
 from .kv_block_pool import KVBlockPool
 from .kv_runtime import KVRuntimeContext, PrefillChunkContext, PrefillRuntimeContext
 from .model import MiniGPT
@@ -68,28 +70,38 @@ class ModelRunner:
 
     # -------------------------------------------------------------- decode
 
+    def _reserve_decode_rows(self, sequences: list[SequenceState]):
+        """Reserves this step's slot per sequence; returns the metadata rows."""
+        slots = [self.block_manager.reserve_append_slot(seq)[2] for seq in sequences]
+        return ([seq.last_token for seq in sequences], [seq.length for seq in sequences], slots,
+                [seq.block_table for seq in sequences])
+
     def _prepare_decode_batch(self, sequences: list[SequenceState]):
         B = len(sequences)
         assert B > 0
-        slots = [self.block_manager.reserve_append_slot(seq)[2] for seq in sequences]
-        M = max(len(seq.block_table) for seq in sequences)
-        # [input_ids | positions | context_lengths | slot_mapping | block_tables]
-        host = torch.full((4 * B + B * M,), -1, dtype=torch.long)
-        host[0:B] = torch.tensor([seq.last_token for seq in sequences], dtype=torch.long)
-        host[B:2 * B] = torch.tensor([seq.length for seq in sequences], dtype=torch.long)
-        host[2 * B:3 * B] = host[B:2 * B] + 1
-        host[3 * B:4 * B] = torch.tensor(slots, dtype=torch.long)
-        tables = host[4 * B:].view(B, M)
-        for b, seq in enumerate(sequences):
-            tables[b, :len(seq.block_table)] = torch.tensor(seq.block_table, dtype=torch.long)
-        dev = host.to(self.device)
-        metadata = DecodeBatchMetadata(
-            positions=dev[B:2 * B],
-            context_lengths=dev[2 * B:3 * B],
-            block_tables=dev[4 * B:].view(B, M),
-            slot_mapping=dev[3 * B:4 * B],
-        )
-        return dev[0:B].view(B, 1), metadata
+        tokens, positions, slots, tables = self._reserve_decode_rows(sequences)
+        M = max(len(t) for t in tables)
+        dev = pack_decode_metadata(tokens, positions, slots, tables, B, M).to(self.device)
+        return metadata_views(dev, B, M)
+
+    def enable_decode_graphs(self, max_blocks_per_seq: int | None = None,
+                             buckets: tuple[int, ...] | None = None) -> None:
+        """Replays decode steps from HIP graphs captured per batch-size bucket.
+
+        Needs the model on a GPU with the hip decode backend. The block-table
+        width is fixed at ``max_blocks_per_seq`` (default: the model's
+        position limit in blocks); steps that do not fit a bucket run eagerly.
+        """
+        M = max_blocks_per_seq or -(-self.model.block_size // self.kv_pool.block_size)
+        self._decode_graphs = DecodeGraphs(self.model, self.kv_pool, M,
+                                           buckets if buckets is not None else DEFAULT_BUCKETS)
+
+    def capture_decode_graphs(self, batch_sizes) -> None:
+        """Captures the buckets for these batch sizes now (e.g. before timing)."""
+        for B in batch_sizes:
+            b = self._decode_graphs.bucket(B)
+            if b is not None:
+                self._decode_graphs.capture(b)
 
     def decode_one(self, seq: SequenceState) -> int:
         """Serial one-sequence decode; returns the greedy next token."""
@@ -106,6 +118,20 @@ class ModelRunner:
     def decode_batch(self, sequences: list[SequenceState]):
         if not sequences:
             return []
+        graphs = getattr(self, "_decode_graphs", None)
+        if graphs is not None:
+            rows = self._reserve_decode_rows(sequences)
+            out = graphs.run(*rows)
+            if out is None:  # no bucket fits: run this step eagerly with the same slots
+                B, M = len(sequences), max(len(t) for t in rows[3])
+                dev = pack_decode_metadata(*rows, B, M).to(self.device)
+                input_ids, metadata = metadata_views(dev, B, M)
+                logits = self.model.decode_batch(input_ids=input_ids, metadata=metadata, kv_pool=self.kv_pool)
+                last = logits[:, -1, :]
+                out = (last, torch.argmax(last, dim=-1).tolist())
+            for seq in sequences:
+                seq.length += 1
+            return out
         input_ids, metadata = self._prepare_decode_batch(sequences=sequences)
         logits = self.model.decode_batch(input_ids=input_ids, metadata=metadata, kv_pool=self.kv_pool)
         for seq in sequences:
