@@ -17,6 +17,7 @@ record.
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from .decode_batch_metadata import DecodeBatchMetadata
@@ -29,18 +30,20 @@ def pack_decode_metadata(tokens, positions, slots, tables, B_pad: int, M: int) -
     """Host int64 buffer [ids | positions | context_lengths | slots | tables]
     for B_pad rows (rows past len(tokens) are padding) and table width M."""
     B = len(tokens)
-    host = torch.full((4 * B_pad + B_pad * M,), -1, dtype=torch.long)
-    host[0:B_pad] = 0
-    host[B_pad:3 * B_pad] = 0
-    host[0:B] = torch.tensor(tokens, dtype=torch.long)
-    host[B_pad:B_pad + B] = torch.tensor(positions, dtype=torch.long)
-    host[2 * B_pad:2 * B_pad + B] = host[B_pad:B_pad + B] + 1
-    host[3 * B_pad:3 * B_pad + B] = torch.tensor(slots, dtype=torch.long)
-    view = host[4 * B_pad:].view(B_pad, M)
-    for b, table in enumerate(tables):
-        if table:
-            view[b, :len(table)] = torch.tensor(table, dtype=torch.long)
-    return host
+    host = np.full(4 * B_pad + B_pad * M, -1, dtype=np.int64)
+    host[:3 * B_pad] = 0
+    if B:
+        host[:B] = tokens
+        host[B_pad:B_pad + B] = positions
+        host[2 * B_pad:2 * B_pad + B] = host[B_pad:B_pad + B] + 1
+        host[3 * B_pad:3 * B_pad + B] = slots
+        lens = np.fromiter((len(t) for t in tables), dtype=np.int64, count=B)
+        n = int(lens.sum())
+        flat = np.fromiter((x for t in tables for x in t), dtype=np.int64, count=n)
+        starts = np.repeat(np.cumsum(lens) - lens, lens)
+        rows = np.repeat(np.arange(B, dtype=np.int64), lens)
+        host[4 * B_pad + rows * M + (np.arange(n, dtype=np.int64) - starts)] = flat
+    return torch.from_numpy(host)
 
 
 def metadata_views(buf: torch.Tensor, B_pad: int, M: int):

@@ -349,3 +349,22 @@ def test_reference_backend_skips_padding_slots():
         model.decode_batch(torch.tensor([[1], [2]]), meta, pool)
     assert torch.equal(pool.k[:, 0], before[:, 0])            # padded row wrote nothing
     assert not torch.equal(pool.k[:, 1, 0], before[:, 1, 0])  # the other row did
+
+
+def test_pack_decode_metadata_matches_row_by_row_construction():
+    from minivllm.decode_graphs import metadata_views, pack_decode_metadata
+
+    rng = random.Random(5)
+    B, B_pad, M = 5, 8, 12
+    tables = [[rng.randrange(100) for _ in range(rng.randint(1, M))] for _ in range(B)]
+    tokens = [rng.randrange(50) for _ in range(B)]
+    positions = [rng.randrange(1, 200) for _ in range(B)]
+    slots = [rng.randrange(1600) for _ in range(B)]
+    buf = pack_decode_metadata(tokens, positions, slots, tables, B_pad, M)
+    ids, meta = metadata_views(buf, B_pad, M)
+    assert ids[:, 0].tolist() == tokens + [0] * (B_pad - B)
+    assert meta.positions.tolist() == positions + [0] * (B_pad - B)
+    assert meta.context_lengths.tolist() == [p + 1 for p in positions] + [0] * (B_pad - B)
+    assert meta.slot_mapping.tolist() == slots + [-1] * (B_pad - B)
+    want = [t + [-1] * (M - len(t)) for t in tables] + [[-1] * M] * (B_pad - B)
+    assert meta.block_tables.tolist() == want
