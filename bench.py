@@ -124,15 +124,15 @@ def copy_line(mib: int, dev, reps: int = 3):
     return {"mib": mib, "ms": round(ms, 4), "gbps_read_plus_write": round(2 * src.numel() / (ms * 1e-3) / 1e9, 1)}
 
 
-def e2e_line(n_requests: int, dev, graphs: bool):
-    """The full runtime under recompute preemption with the HIP decode backend;
-    with `graphs`, decode steps replay HIP graphs captured (before timing) for
-    every batch bucket up to max_running."""
+def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2"):
+    """The full runtime under recompute preemption with the HIP decode backend
+    and the given prefill mode; with `graphs`, decode steps replay HIP graphs
+    captured (before timing) for every batch bucket up to max_running."""
     import torch
 
     import _e2e
 
-    spec = _e2e.RuntimeSpec(n_requests=n_requests)
+    spec = _e2e.RuntimeSpec(n_requests=n_requests, prefill_mode=prefill_mode)
     prompts = _e2e.make_prompts(spec)
     model = _e2e.make_model(spec, dev, torch.bfloat16)
     model.set_decode_attention_backend("hip")
@@ -156,10 +156,49 @@ def e2e_line(n_requests: int, dev, graphs: bool):
     stats.update({"requests": n_requests, "pool_blocks": _e2e.pool_blocks(spec, prompts),
                   "sum_prompt_tokens": sum(len(p) for p in prompts),
                   "model": "MiniGPT dim 2048, 16 heads, 12 layers, vocab 32000, bf16, random init (seed 0)",
-                  "schedule": "max_running 256, token budget 2048, recompute preemption, prefill sdpa_v2",
+                  "schedule": "max_running 256, token budget 2048, recompute preemption",
+                  "prefill_mode": prefill_mode,
                   "decode_backend": "hip", "decode_graphs": graphs,
                   "tokens": [s.generated_tokens for s in seqs]})
     return stats
+
+
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def prefill_line(dev, start: int, T: int, H: int = 16, D: int = 128, steps: int = 20):
+    """Paged prefill attention of one bf16 chunk (T queries after a cached
+    prefix of `start` tokens, block size 16, scattered table): the HIP kernel
+    against the fp32 gather + SDPA of prefill mode sdpa_v2 on the same GPU.
+    FLOPs are the causal algorithmic count 4*H*D*sum_i (start + i + 1)."""
+    import types
+
+    import torch
+
+    from minivllm import hip_paged_decode as hpd
+    from minivllm.attention import KVCacheCausalSelfAttention
+    from minivllm.kv_block_pool import KVBlockPool
+
+    S = 16
+    n_blocks = -(-(start + T) // S)
+    N = n_blocks + 64
+    g = torch.Generator().manual_seed(1)
+    table = torch.randperm(N, generator=g)[:n_blocks]
+    pool = KVBlockPool(1, N, S, H, D, device=dev, dtype=torch.bfloat16)
+    pool.k.normal_()
+    pool.v.normal_()
+    qkv = torch.randn(1, T, 3, H, D, device=dev).to(torch.bfloat16)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    tdev = table.to(dev)
+    hip_ms = time_steps(lambda: hpd.paged_prefill_hip(q[0], pool, tdev, start, 0), steps, 3)
+    attn = KVCacheCausalSelfAttention(H * D, H, start + T).to(dev)
+    seq = types.SimpleNamespace(block_table=table.tolist())
+    sdpa_ms = time_steps(lambda: attn._dense_prefill(q, k, v, start, pool, seq, 0), max(3, steps // 4), 1)
+    flops = 4 * H * D * (T * start + T * (T + 1) // 2)
+    tflops = flops / (hip_ms * 1e-3) / 1e12
+    return {"start": start, "T": T, "H": H, "D": D, "us": round(hip_ms * 1e3, 2),
+            "tflops": round(tflops, 1), "pct_of_bf16_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+            "sdpa_v2_fp32_us": round(sdpa_ms * 1e3, 1), "speedup_vs_sdpa_v2": round(sdpa_ms / hip_ms, 1)}
 
 
 def attention_speedup_grid(dev):
@@ -324,17 +363,28 @@ def main() -> None:
             log(f"extra e2e speedup: {extras['e2e_small_model_speedup']}")
             torch.cuda.empty_cache()
 
+        if not args.no_extras or args.e2e:
+            for start, T in ((0, 512), (2048, 2048)):
+                key = f"prefill_bf16_start{start}_T{T}_H16_D128"
+                extras[key] = prefill_line(dev, start, T)
+                log(f"extra {key}: {extras[key]}")
+            torch.cuda.empty_cache()
+
         if args.e2e:
-            for graphs in (False, True):
-                key = "e2e_runtime_bf16_preemption" + ("_graphs" if graphs else "")
-                log(f"end-to-end runtime, {args.e2e_requests} requests, decode graphs {graphs}")
-                extras[key] = e2e_line(args.e2e_requests, dev, graphs)
+            runs = (("e2e_runtime_bf16_preemption", False, "sdpa_v2"),
+                    ("e2e_runtime_bf16_preemption_hip_prefill", False, "hip"),
+                    ("e2e_runtime_bf16_preemption_hip_prefill_graphs", True, "hip"))
+            for key, graphs, mode in runs:
+                log(f"end-to-end runtime, {args.e2e_requests} requests, prefill {mode}, decode graphs {graphs}")
+                extras[key] = e2e_line(args.e2e_requests, dev, graphs, mode)
                 torch.cuda.empty_cache()
-            eager, graph = extras["e2e_runtime_bf16_preemption"], extras["e2e_runtime_bf16_preemption_graphs"]
-            same = sum(a == b for a, b in zip(eager.pop("tokens"), graph.pop("tokens")))
-            graph["identical_token_streams_vs_eager"] = f"{same}/{args.e2e_requests}"
-            log(f"e2e: eager {eager}")
-            log(f"e2e: graphs {graph}")
+            base = extras[runs[0][0]]["tokens"]
+            for key, _, _ in runs[1:]:
+                same = sum(a == b for a, b in zip(base, extras[key]["tokens"]))
+                extras[key]["identical_token_streams_vs_first"] = f"{same}/{args.e2e_requests}"
+            for key, _, _ in runs:
+                extras[key].pop("tokens")
+                log(f"e2e {key}: {extras[key]}")
 
         if args.calibrate_copy_mib:
             extras["copy_calibration"] = copy_line(args.calibrate_copy_mib, dev, reps=3)

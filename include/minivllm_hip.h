@@ -141,6 +141,38 @@ int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D,
                                       int64_t S, int64_t M,
                                       int64_t split_tokens);
 
+/*
+ * Paged prefill attention of one chunk of one sequence.
+ * Replaces the per-token prefill loop of
+ * KVCacheCausalSelfAttention.forward_prefill_chunk
+ * (minivllm/attention.py:269-299, paged_attention_online per query) and the
+ * prefix-aware gather + SDPA of mode sdpa_v2 (minivllm/attention.py:229-267).
+ *
+ * The chunk holds T query rows at absolute positions start_pos .. start_pos+T-1;
+ * its own K/V rows must already be in the pool (mgi_kv_append on the same
+ * stream). For t < T, h < H:
+ *   out[t,h,:] = sum_j softmax_j(scale * q[t,h,:] . K[j,h,:]) * V[j,h,:]
+ * over the logical tokens j = 0 .. start_pos + t, where token j lives in
+ * physical block block_table[j / S] at offset j % S of layer layer_idx.
+ * block_table must hold n_blocks >= ceil((start_pos + T) / S) entries; only
+ * those are read. An entry outside [0, N) is treated as a fully masked block.
+ * q, out and the pool share one dtype; arithmetic is fp32 (bf16 inputs run
+ * on the bf16 matrix cores with P rounded to bf16 for the PV product).
+ * Layouts: q, out [T, H, D] (any strides); block_table [n_blocks] with
+ * element stride bt_stride.
+ */
+int mgi_paged_prefill(void* out, const int64_t* out_strides, /* [3] */
+                      const void* q, const int64_t* q_strides, /* [3] */
+                      const void* k_pool, const void* v_pool,
+                      const int64_t* k_pool_strides, /* [5] */
+                      const int64_t* v_pool_strides, /* [5] */
+                      int dtype,
+                      const void* block_table, int64_t bt_stride, int bt_itype,
+                      int64_t n_blocks, int64_t start_pos, int64_t T,
+                      int64_t H, int64_t D, int64_t S, int64_t N,
+                      int64_t L, int64_t layer_idx, float scale,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

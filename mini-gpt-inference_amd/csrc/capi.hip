@@ -324,4 +324,130 @@ int mgi_kv_append(void* k_pool, void* v_pool, const int64_t* k_pool_strides,
   return MGI_OK;
 }
 
+int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
+                      const int64_t* q_strides, const void* k_pool, const void* v_pool,
+                      const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
+                      const void* block_table, int64_t bt_stride, int bt_itype, int64_t n_blocks,
+                      int64_t start_pos, int64_t T, int64_t H, int64_t D, int64_t S, int64_t N,
+                      int64_t L, int64_t layer_idx, float scale, void* stream) {
+  using namespace mgi;
+  g_err.clear();
+  if (T < 0) return fail(MGI_EINVAL, "row count must be non-negative");
+  if (T == 0) return MGI_OK;
+  if (!out || !q || !k_pool || !v_pool || !block_table) return fail(MGI_EINVAL, "null tensor pointer");
+  if (!out_strides || !q_strides || !k_pool_strides || !v_pool_strides)
+    return fail(MGI_EINVAL, "null stride array");
+  if (H <= 0 || D <= 0) return fail(MGI_EINVAL, "q dimensions must be nonzero");
+  if (S <= 0 || N <= 0 || L <= 0) return fail(MGI_EINVAL, "pool dimensions must be nonzero");
+  if (layer_idx < 0 || layer_idx >= L) return fail(MGI_EINVAL, "layer_idx outside KV pool");
+  if (start_pos < 0) return fail(MGI_EINVAL, "start_pos must be non-negative");
+  if (n_blocks < (start_pos + T + S - 1) / S)
+    return fail(MGI_EINVAL, "block table shorter than ceil((start_pos + T) / S)");
+  if (!valid_dtype(dtype)) return fail(MGI_EINVAL, "unknown dtype code");
+  if (!valid_itype(bt_itype)) return fail(MGI_EINVAL, "block_table must be int32 or int64");
+  if (!std::isfinite(scale)) return fail(MGI_EINVAL, "scale must be finite");
+  if (!nonneg(out_strides, 3) || !nonneg(q_strides, 3) || !nonneg(k_pool_strides, 5) ||
+      !nonneg(v_pool_strides, 5) || bt_stride < 0)
+    return fail(MGI_EINVAL, "strides must be non-negative");
+  if (start_pos + T >= (int64_t(1) << 31)) return fail(MGI_EUNSUPPORTED, "start_pos + T must be < 2^31");
+  if (H > kMaxGridYZ) return fail(MGI_EUNSUPPORTED, "more than 65535 heads");
+  if (D > 512) return fail(MGI_EUNSUPPORTED, "head_dim larger than 512");
+
+  const int64_t eb = dtype_bytes(dtype);
+  const char* kbase = static_cast<const char*>(k_pool) + layer_idx * k_pool_strides[0] * eb;
+  const char* vbase = static_cast<const char*>(v_pool) + layer_idx * v_pool_strides[0] * eb;
+  const bool bf16 = dtype == MGI_BF16;
+  const int dp = (dtype == MGI_BF16 || dtype == MGI_F32) ? prefill_head_dim_bucket(bf16, (int)D) : 0;
+
+  // Matrix-core path: bf16 or f32, head dim a multiple of one 16-byte chunk
+  // within the padded bucket, unit head-dim strides, 16-byte aligned rows.
+  const bool mfma = dp != 0 && D % (16 / eb) == 0 && q_strides[2] == 1 && out_strides[2] == 1 &&
+                    k_pool_strides[4] == 1 && v_pool_strides[4] == 1 && aligned16(q) &&
+                    aligned16(out) && aligned16(kbase) && aligned16(vbase) &&
+                    mult16(q_strides[0], eb) && mult16(q_strides[1], eb) &&
+                    mult16(out_strides[0], eb) && mult16(out_strides[1], eb) &&
+                    mult16(k_pool_strides[1], eb) && mult16(k_pool_strides[2], eb) &&
+                    mult16(k_pool_strides[3], eb) && mult16(v_pool_strides[1], eb) &&
+                    mult16(v_pool_strides[2], eb) && mult16(v_pool_strides[3], eb) &&
+                    N < (int64_t(1) << 31);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (mfma) {
+    PrefillArgs a{};
+    a.out = out;
+    a.o_st = out_strides[0];
+    a.o_sh = out_strides[1];
+    a.q = q;
+    a.q_st = q_strides[0];
+    a.q_sh = q_strides[1];
+    a.k = kbase;
+    a.v = vbase;
+    a.k_sn = k_pool_strides[1];
+    a.k_ss = k_pool_strides[2];
+    a.k_sh = k_pool_strides[3];
+    a.v_sn = v_pool_strides[1];
+    a.v_ss = v_pool_strides[2];
+    a.v_sh = v_pool_strides[3];
+    a.bt = block_table;
+    a.bt_s = bt_stride;
+    a.bt_i64 = bt_itype == MGI_I64;
+    a.start = (int)start_pos;
+    a.T = (int)T;
+    a.H = (int)H;
+    a.D = (int)D;
+    a.S = (int)S;
+    a.s_shift = (S & (S - 1)) == 0 ? __builtin_ctzll((unsigned long long)S) : -1;
+    a.N = N;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    // Four wavefronts (64 query rows) per workgroup once that still fills
+    // the chip; two otherwise.
+    const int waves = ((T + 63) / 64) * H >= device_cus() ? 4 : 2;
+    e = launch_paged_prefill(a, bf16, dp, waves, st);
+  } else {
+    // Any other shape: the chunk as T single-query rows of the generic decode
+    // kernel, sharing one table row, with context lengths start_pos + t + 1.
+    if (T > kMaxGridYZ) return fail(MGI_EUNSUPPORTED, "chunk longer than 65535 rows for this shape");
+    if (n_blocks * S >= (int64_t(1) << 31)) return fail(MGI_EUNSUPPORTED, "n_blocks*S must be < 2^31");
+    DecodeArgs a{};
+    a.out = out;
+    a.o_sb = out_strides[0];
+    a.o_sh = out_strides[1];
+    a.o_sd = out_strides[2];
+    a.q = q;
+    a.q_sb = q_strides[0];
+    a.q_sh = q_strides[1];
+    a.q_sd = q_strides[2];
+    a.k = kbase;
+    a.v = vbase;
+    a.k_sn = k_pool_strides[1];
+    a.k_ss = k_pool_strides[2];
+    a.k_sh = k_pool_strides[3];
+    a.k_sd = k_pool_strides[4];
+    a.v_sn = v_pool_strides[1];
+    a.v_ss = v_pool_strides[2];
+    a.v_sh = v_pool_strides[3];
+    a.v_sd = v_pool_strides[4];
+    a.bt = block_table;
+    a.bt_sb = 0;
+    a.bt_sm = bt_stride;
+    a.cl = nullptr;
+    a.ctx_base = start_pos;
+    a.bt_i64 = bt_itype == MGI_I64;
+    a.B = (int)T;
+    a.H = (int)H;
+    a.D = (int)D;
+    a.S = (int)S;
+    a.M = (int)n_blocks;
+    a.N = N;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.part_tokens = (int)(n_blocks * S);
+    a.max_parts = 1;
+    DecodePlan plan{};
+    plan.path = DecodePath::kGeneric;
+    e = launch_paged_decode(a, dtype, plan, st);
+  }
+  if (e != hipSuccess) return fail(MGI_ELAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
+  return MGI_OK;
+}
+
 }  // extern "C"

@@ -21,8 +21,9 @@ struct DecodeArgs {
   int64_t v_sn, v_ss, v_sh, v_sd;
   const void* bt;
   int64_t bt_sb, bt_sm;
-  const void* cl;
+  const void* cl;      // null: row b's context length is ctx_base + b + 1
   int64_t cl_s;
+  int64_t ctx_base;
   int bt_i64, cl_i64;
   int B, H, D, S, M;
   int64_t N;
@@ -50,6 +51,28 @@ struct AppendArgs {
   int64_t N;
 };
 
+// Paged prefill attention of one chunk: query row i (absolute position
+// start + i) attends keys 0 .. start + i through one block-table row. Pool
+// pointers already point at layer layer_idx; strides are in elements and the
+// head dim is contiguous everywhere.
+struct PrefillArgs {
+  void* out;
+  int64_t o_st, o_sh;
+  const void* q;
+  int64_t q_st, q_sh;
+  const void* k;
+  const void* v;
+  int64_t k_sn, k_ss, k_sh;
+  int64_t v_sn, v_ss, v_sh;
+  const void* bt;
+  int64_t bt_s;
+  int bt_i64;
+  int start, T, H, D, S;
+  int s_shift;        // log2(S) when S is a power of two, else -1
+  int64_t N;
+  float scale_log2;   // softmax scale * log2(e)
+};
+
 enum class DecodePath { kFast, kGeneric };
 
 // Paged decode: how a call will run (decided from dtype, shapes, strides and
@@ -63,6 +86,13 @@ struct DecodePlan {
 
 hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan& plan,
                                hipStream_t stream);
+
+// Paged prefill on the matrix cores. `dp` is the padded head dim returned by
+// prefill_head_dim_bucket (0: no MFMA variant); `waves` is 2 or 4 (16 query
+// rows per wavefront).
+int prefill_head_dim_bucket(int dtype_is_bf16, int D);
+hipError_t launch_paged_prefill(const PrefillArgs& a, bool bf16, int dp, int waves,
+                                hipStream_t stream);
 
 // KV append launchers. `vector_path` copies 16-byte chunks (same dtype,
 // contiguous aligned rows); otherwise an element loop converts dtypes.

@@ -111,7 +111,7 @@ template <> struct QFrag<float> {
 
 template <typename T>
 __device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int b) {
-  const int64_t c = load_index(a.cl, a.cl_i64, (int64_t)b * a.cl_s);
+  const int64_t c = a.cl ? load_index(a.cl, a.cl_i64, (int64_t)b * a.cl_s) : a.ctx_base + b + 1;
   const int64_t max_ctx = (int64_t)a.M * a.S;
   return (int)(c < 0 ? 0 : (c > max_ctx ? max_ctx : c));
 }

@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "mgi_paged_decode",
     "mgi_paged_decode_workspace_bytes",
     "mgi_paged_decode_split_tokens",
+    "mgi_paged_prefill",
 )
 
 _lock = threading.Lock()
@@ -73,6 +74,17 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mgi_paged_decode_workspace_bytes.argtypes = [_i64] * 6
     lib.mgi_paged_decode_split_tokens.restype = _i64
     lib.mgi_paged_decode_split_tokens.argtypes = [_i64] * 6
+    lib.mgi_paged_prefill.restype = _i
+    lib.mgi_paged_prefill.argtypes = [
+        _p, _pi64,                         # out, strides
+        _p, _pi64,                         # q, strides
+        _p, _p, _pi64, _pi64, _i,          # pools, strides, dtype
+        _p, _i64, _i, _i64,                # block table, stride, itype, entries
+        _i64, _i64,                        # start_pos, T
+        _i64, _i64, _i64, _i64, _i64, _i64,  # H D S N L layer
+        ctypes.c_float,                    # scale
+        _p,                                # stream
+    ]
 
 
 def lib() -> ctypes.CDLL:

@@ -21,7 +21,11 @@ Prefill attention (``set_prefill_fastpath_mode``): "reference" attends each
 query token through the pool with paged_attention_online; "sdpa_v1" /
 "sdpa_v2" use scaled_dot_product_attention over the chunk (and, for v2, the
 gathered cached prefix) with an absolute-position causal mask. The SDPA
-paths run in float32 for every model dtype.
+paths run in float32 for every model dtype. "hip" runs every chunk (first or
+later) through the paged prefill kernel of libminivllm_hip.so, which reads
+the cached prefix and the chunk straight from the pool after the chunk's
+KV append (minivllm.hip_paged_decode.paged_prefill_hip, imported at call
+time); it needs the model and pool on a GPU and raises otherwise.
 """
 from __future__ import annotations
 
@@ -40,6 +44,7 @@ from .paged_attention_v1_reference import paged_attention_online
 
 DECODE_BACKENDS = ("reference", "hip", "triton_v0")
 HIP_BACKENDS = ("hip", "triton_v0")
+PREFILL_MODES = ("reference", "sdpa_v1", "sdpa_v2", "hip")
 
 
 @dataclass
@@ -88,6 +93,7 @@ class KVCacheCausalSelfAttention(nn.Module):
         self.dropout = dropout
         self.prefill_fastpath_enabled = False
         self.prefill_prefix_fastpath_enabled = False
+        self.prefill_hip = False
         self.decode_attention_backend = "reference"
         self.qkv = nn.Linear(n_embd, 3 * n_embd, bias=False)
         self.register_buffer("tril", torch.tril(torch.ones(block_size, block_size)))
@@ -141,6 +147,24 @@ class KVCacheCausalSelfAttention(nn.Module):
             values.transpose(1, 2).float().contiguous(), attn_mask=mask, dropout_p=0.0)
         return out.transpose(1, 2).reshape(1, T, H * D).to(q.dtype)
 
+    def _hip_prefill(self, q: Tensor, start: int, pool: KVBlockPool, seq, layer_idx: int,
+                     table: Tensor | None) -> Tensor:
+        """Chunk queries [1, T, H, D] at positions start.. through the paged
+        prefill kernel; the chunk's KV is already in the pool."""
+        from .hip_paged_decode import paged_prefill_hip
+
+        _, T, H, D = q.shape
+        if torch.is_grad_enabled() and q.requires_grad:
+            raise RuntimeError("hip prefill is inference-only; run under torch.inference_mode()")
+        if table is None:
+            n_blocks = -(-(start + T) // pool.block_size)
+            ids = seq.block_table[:n_blocks]
+            if len(ids) != n_blocks:
+                raise RuntimeError("incomplete KV block table for prefix")
+            table = torch.tensor(ids, dtype=torch.long, device=q.device)
+        out = paged_prefill_hip(q[0], pool, table, start, layer_idx)
+        return out.reshape(1, T, H * D)
+
     # ------------------------------------------------------------- prefill
 
     def forward_prefill(self, x: Tensor, context: PrefillRuntimeContext) -> Tensor:
@@ -150,6 +174,12 @@ class KVCacheCausalSelfAttention(nn.Module):
         assert len(context.slot_mapping) == T
         q, k, v = self._qkv_heads(x)
         self._write_chunk_kv(k[0], v[0], context.kv_pool, context.layer_idx, context.slot_mapping)
+        if self.prefill_hip:
+            if context.start_pos != 0:
+                raise ValueError("whole-prompt prefill starts at position 0")
+            out = self._hip_prefill(q, 0, context.kv_pool, context.seq_state,
+                                    context.layer_idx, context.block_table)
+            return self._finish(out)
         out = self._dense_prefill(q, k, v, 0, context.kv_pool, context.seq_state, context.layer_idx)
         return self._finish(out)
 
@@ -161,6 +191,9 @@ class KVCacheCausalSelfAttention(nn.Module):
         pool, layer = context.kv_pool, context.layer_idx
         self._write_chunk_kv(k[0], v[0], pool, layer, context.slot_mapping)
         start = context.start_pos
+        if self.prefill_hip:
+            out = self._hip_prefill(q, start, pool, context.seq_state, layer, context.block_table)
+            return self._finish(out)
         if self.prefill_fastpath_enabled and (start == 0 or self.prefill_prefix_fastpath_enabled):
             out = self._dense_prefill(q, k, v, start, pool, context.seq_state, layer)
             return self._finish(out)

@@ -1,4 +1,5 @@
-"""MI355X HIP paged decode backend: fused decode attention and KV append.
+"""MI355X HIP paged KV backend: fused decode attention, KV append and paged
+prefill attention.
 
 Drop-in for minivllm/triton_paged_decode.py. Inputs match
 paged_attention_batch_online_v1:
@@ -17,6 +18,11 @@ these functions raise.
 
 Beyond the Triton v0 backend: float32, bfloat16 and float16; head_dim up to
 512; any block size; split-context partitions for long contexts.
+
+paged_prefill_hip is the prefill counterpart (the reference's per-token
+loop, minivllm/attention.py:269-299, and its sdpa_v2 gather,
+minivllm/attention.py:229-267): causal attention of one chunk's queries over
+the sequence's cached prefix and the chunk itself, read from the pool.
 """
 from __future__ import annotations
 
@@ -142,3 +148,59 @@ def kv_append(pool: KVBlockPool, layer_idx: int, k: torch.Tensor, v: torch.Tenso
         _native.stream_handle(pool.k.device),
     )
     _native.check(status)
+
+
+def paged_prefill_hip(q: torch.Tensor, pool: KVBlockPool, block_table: torch.Tensor,
+                      start_pos: int, layer_idx: int) -> torch.Tensor:
+    """Causal attention of a chunk's queries through the paged pool.
+
+    q: [T, H, D] (any strides), query row t at absolute position start_pos + t.
+    block_table: [n] integer tensor of the sequence's physical blocks,
+    n >= ceil((start_pos + T) / S). The chunk's own K/V must already be in
+    the pool (kv_append on the same stream). Returns a fresh [T, H, D]
+    tensor of q.dtype with out[t] = softmax(q[t] K[0..start_pos+t]^T / sqrt(D)) V.
+    """
+    lib = _native.lib()
+    _check_device(q, "q")
+    if q.ndim != 3:
+        raise ValueError("q must have shape [T,H,D]")
+    t, h, d = q.shape
+    if h == 0 or d == 0:
+        raise ValueError("q dimensions must be nonzero")
+    if d > 512:
+        raise ValueError("HIP backend supports head_dim <= 512")
+    if q.dtype not in _FLOATS:
+        raise ValueError("q must be float32, bfloat16 or float16")
+    if pool.k.dtype != q.dtype or pool.v.dtype != q.dtype:
+        raise ValueError("KV pool dtype must match q dtype")
+    if pool.k.ndim != 5 or pool.v.shape != pool.k.shape:
+        raise ValueError("KV tensors must have matching [L,P,S,H,D] shape")
+    L, N, S, H, D = pool.k.shape
+    if (H, D) != (h, d):
+        raise ValueError("KV head dimensions do not match q")
+    if block_table.ndim != 1 or block_table.dtype not in _INDEX:
+        raise ValueError("block_table must be a 1-D integer tensor")
+    if start_pos < 0:
+        raise ValueError("start_pos must be non-negative")
+    if block_table.shape[0] < -(-(start_pos + t) // S):
+        raise ValueError("block_table shorter than ceil((start_pos + T) / S)")
+    if not 0 <= layer_idx < L:
+        raise ValueError("layer_idx outside KV pool")
+    if any(x.device != q.device for x in (pool.k, pool.v, block_table)):
+        raise ValueError("all inputs must reside on same GPU device")
+    out = torch.empty((t, h, d), dtype=q.dtype, device=q.device)
+    if t == 0:
+        return out
+    status = lib.mgi_paged_prefill(
+        out.data_ptr(), _native.strides(out),
+        q.data_ptr(), _native.strides(q),
+        pool.k.data_ptr(), pool.v.data_ptr(), _native.strides(pool.k), _native.strides(pool.v),
+        _native.DTYPE_CODES[q.dtype],
+        block_table.data_ptr(), block_table.stride(0), _native.ITYPE_CODES[block_table.dtype],
+        block_table.shape[0], int(start_pos), t,
+        h, d, S, N, L, int(layer_idx),
+        1.0 / math.sqrt(d),
+        _native.stream_handle(q.device),
+    )
+    _native.check(status)
+    return out

@@ -26,13 +26,19 @@ class KVRuntimeContext:
 
 @dataclass
 class PrefillRuntimeContext:
-    """Whole-prompt prefill of one layer."""
+    """Whole-prompt prefill of one layer.
+
+    block_table optionally carries the sequence's first
+    ceil(context_length / S) physical blocks as an integer tensor on the
+    pool's device (the HIP prefill kernel reads it; built once per call).
+    """
     seq_state: SequenceState
     kv_pool: KVBlockPool
     layer_idx: int
     start_pos: int
     context_length: int
-    slot_mapping: list[int]
+    slot_mapping: list[int] | torch.Tensor
+    block_table: torch.Tensor | None = None
 
 
 @dataclass
@@ -41,6 +47,8 @@ class PrefillChunkContext:
 
     slot_mapping is a list of physical slots, or the same slots as an int64
     tensor on the pool's device (the runner moves them once per chunk).
+    block_table optionally carries the sequence's first
+    ceil((start_pos + num_tokens) / S) physical blocks as a device tensor.
     """
     seq_state: SequenceState
     kv_pool: KVBlockPool
@@ -48,3 +56,4 @@ class PrefillChunkContext:
     start_pos: int
     num_tokens: int
     slot_mapping: list[int] | torch.Tensor
+    block_table: torch.Tensor | None = None

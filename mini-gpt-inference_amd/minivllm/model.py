@@ -12,7 +12,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 from torch.utils.checkpoint import checkpoint
 
-from .attention import DECODE_BACKENDS, KVCache
+from .attention import DECODE_BACKENDS, PREFILL_MODES, KVCache
 from .block import TransformerBlock
 from .decode_batch_metadata import DecodeBatchMetadata
 from .kv_block_pool import KVBlockPool
@@ -43,14 +43,18 @@ class MiniGPT(nn.Module):
         for block in self.blocks:
             block.attn.prefill_fastpath_enabled = enabled
             block.attn.prefill_prefix_fastpath_enabled = False
+            block.attn.prefill_hip = False
 
     def set_prefill_fastpath_mode(self, mode: str) -> None:
-        """'reference', 'sdpa_v1' (first chunk) or 'sdpa_v2' (prefix-aware)."""
-        if mode not in ("reference", "sdpa_v1", "sdpa_v2"):
-            raise ValueError("mode must be reference, sdpa_v1 or sdpa_v2")
+        """'reference', 'sdpa_v1' (first chunk), 'sdpa_v2' (prefix-aware) or
+        'hip' (every chunk through the paged prefill kernel of
+        libminivllm_hip.so, any model dtype; GPU only)."""
+        if mode not in PREFILL_MODES:
+            raise ValueError("mode must be reference, sdpa_v1, sdpa_v2 or hip")
         for block in self.blocks:
             block.attn.prefill_fastpath_enabled = mode != "reference"
-            block.attn.prefill_prefix_fastpath_enabled = mode == "sdpa_v2"
+            block.attn.prefill_prefix_fastpath_enabled = mode in ("sdpa_v2", "hip")
+            block.attn.prefill_hip = mode == "hip"
 
     def set_decode_attention_backend(self, backend: str) -> None:
         """'reference' (PyTorch) or 'hip' (MI355X kernels; 'triton_v0' is an alias).

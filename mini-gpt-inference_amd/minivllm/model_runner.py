@@ -42,8 +42,10 @@ class ModelRunner:
         start = seq.length
         input_ids = torch.tensor([seq.prompt_tokens], device=self.device, dtype=torch.long)
         slots = self.block_manager.reserve_slots(seq, T)
+        slots, table = self._chunk_index_tensors(seq, slots, start + T)
         contexts = [PrefillRuntimeContext(seq_state=seq, kv_pool=self.kv_pool, layer_idx=i,
-                                          start_pos=start, context_length=start + T, slot_mapping=slots)
+                                          start_pos=start, context_length=start + T, slot_mapping=slots,
+                                          block_table=table)
                     for i in range(self.model.n_layer)]
         logits = self.model.prefill(input_ids, contexts)
         seq.length += T
@@ -58,15 +60,25 @@ class ModelRunner:
         assert len(tokens) == num_tokens, "prefill chunk exceeds input prefix"
         input_ids = torch.tensor([tokens], device=self.device, dtype=torch.long)
         slots = self.block_manager.reserve_slots(seq=seq, num_tokens=num_tokens)
-        if self.kv_pool.k.is_cuda:
-            # One host-to-device copy of the chunk's slots, shared by every layer.
-            slots = torch.tensor(slots, dtype=torch.long, device=self.kv_pool.k.device)
+        slots, table = self._chunk_index_tensors(seq, slots, start_pos + num_tokens)
         contexts = [PrefillChunkContext(seq_state=seq, kv_pool=self.kv_pool, layer_idx=i,
-                                        start_pos=start_pos, num_tokens=num_tokens, slot_mapping=slots)
+                                        start_pos=start_pos, num_tokens=num_tokens, slot_mapping=slots,
+                                        block_table=table)
                     for i in range(self.model.n_layer)]
         logits = self.model.prefill_chunk(input_ids=input_ids, contexts=contexts)
         seq.length += num_tokens
         return logits
+
+    def _chunk_index_tensors(self, seq: SequenceState, slots: list[int], context_length: int):
+        """On a GPU pool: the chunk's slots and the sequence's first
+        ceil(context_length / S) table entries in one host-to-device copy,
+        shared by every layer. On the CPU: (slots, None)."""
+        if not self.kv_pool.k.is_cuda:
+            return slots, None
+        n_blocks = -(-context_length // self.kv_pool.block_size)
+        buf = torch.tensor(list(slots) + list(seq.block_table[:n_blocks]), dtype=torch.long)
+        buf = buf.to(self.kv_pool.k.device, non_blocking=False)
+        return buf[:len(slots)], buf[len(slots):]
 
     # -------------------------------------------------------------- decode
 

@@ -18,6 +18,12 @@ Functions and the reference code they restate:
   merge_partials             the split-context merge (no reference function;
                              the per-block merge of paged_attention_batch.py:217-254
                              applied across partitions)
+  paged_prefill              the per-token prefill loop of
+                             minivllm/attention.py:269-299 (query i of a chunk
+                             starting at start_pos runs paged_attention_online,
+                             minivllm/paged_attention_v1_reference.py, with
+                             context_length = start_pos + i + 1), computed as one
+                             dense causal softmax over the gathered tokens
 """
 from __future__ import annotations
 
@@ -235,3 +241,30 @@ def merge_partials(ms: np.ndarray, ls: np.ndarray, Os: np.ndarray) -> np.ndarray
     w = np.exp(ms - M[None, :])
     L = (w * ls).sum(axis=0)
     return (w[..., None] * Os).sum(axis=0) / L[:, None]
+
+
+# ------------------------------------------------------- prefill attention
+
+def paged_prefill(q, k_pool, v_pool, block_table, start: int, layer: int,
+                  scale: float | None = None, acc=np.float64) -> np.ndarray:
+    """Causal attention of chunk queries q [T, H, D] through one block table.
+
+    Query row i sits at absolute position start + i and attends logical
+    tokens 0 .. start + i of the sequence (token j in physical block
+    block_table[j // S], offset j % S of `layer`): the result of the
+    reference's per-token prefill loop (minivllm/attention.py:269-299), which
+    calls paged_attention_online with context_length = start + i + 1. Tokens
+    past start + T - 1 are never read.
+    """
+    q = as_float(q, acc)
+    T, H, D = q.shape
+    sc = _scale(D, scale)
+    ctx = start + T
+    keys, vals = gather_tokens(k_pool, v_pool, np.asarray(block_table)[None, :], ctx, 0, layer, acc)
+    scores = np.einsum("ihd,jhd->hij", q, keys) * sc                      # [H, T, ctx]
+    visible = np.arange(ctx)[None, :] <= (start + np.arange(T))[:, None]  # [T, ctx]
+    scores = np.where(visible[None], scores, -np.inf)
+    scores -= scores.max(axis=-1, keepdims=True)
+    w = np.exp(scores)
+    w /= w.sum(axis=-1, keepdims=True)
+    return np.einsum("hij,jhd->ihd", w, vals)

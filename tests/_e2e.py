@@ -131,13 +131,16 @@ def run_to_completion(rt: MiniRuntime, seqs, max_steps: int = 100000, on_step=No
 GOLDEN_C1 = json.loads((Path(__file__).resolve().parent / "golden" / "c1_greedy_tokens.json").read_text())
 
 
-def run_c1(case: dict, device, backend: str):
-    """Runs one golden case; returns (generated tokens per request, runtime)."""
+def run_c1(case: dict, device, backend: str, prefill_mode: str | None = None):
+    """Runs one golden case; returns (generated tokens per request, runtime).
+
+    prefill_mode overrides the recorded configuration's prefill mode (the
+    golden tokens were produced with it)."""
     cfg = GOLDEN_C1["config"]
     torch.manual_seed(cfg["seed"])
     model = MiniGPT(n_embd=cfg["n_embd"], n_head=cfg["n_head"], vocab_size=cfg["vocab_size"],
                     block_size=cfg["block_size"], dropout=0.0, n_layer=cfg["n_layer"]).eval().to(device)
-    model.set_prefill_fastpath_mode(cfg["prefill_mode"])
+    model.set_prefill_fastpath_mode(prefill_mode or cfg["prefill_mode"])
     model.set_decode_attention_backend(backend)
     B, P, S = case["batch"], case["prompt_len"], cfg["block_size_kv"]
     blocks = B * math.ceil((P + cfg["output_len"] - 1) / S)

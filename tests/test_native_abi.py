@@ -83,6 +83,37 @@ def test_paged_decode_rejects_bad_arguments_on_host():
         assert msg in lib.mgi_last_error().decode(), (kw, lib.mgi_last_error())
 
 
+def test_paged_prefill_rejects_bad_arguments_on_host():
+    lib = _native.lib()
+    st3, st5 = _i64(1, 1, 1), _i64(1, 1, 1, 1, 1)
+    fake = 0x1000  # never dereferenced: every call below fails validation first
+
+    def call(**kw):
+        a = dict(out=fake, q=fake, dtype=_native.MGI_BF16, bt=fake, bt_it=1, n_blocks=2, start=16, T=8,
+                 H=2, D=64, S=16, N=4, L=1, layer=0, scale=0.125)
+        a.update(kw)
+        return lib.mgi_paged_prefill(a["out"], st3, a["q"], st3, fake, fake, st5, st5, a["dtype"],
+                                     a["bt"], 1, a["bt_it"], a["n_blocks"], a["start"], a["T"], a["H"],
+                                     a["D"], a["S"], a["N"], a["L"], a["layer"], a["scale"], None)
+
+    assert call(T=0) == _native.MGI_OK  # nothing to do: no launch
+    cases = [
+        (dict(T=-1), "row count must be non-negative"),
+        (dict(q=None), "null tensor pointer"),
+        (dict(H=0), "q dimensions must be nonzero"),
+        (dict(layer=1), "layer_idx outside KV pool"),
+        (dict(start=-1), "start_pos must be non-negative"),
+        (dict(n_blocks=1), "block table shorter"),
+        (dict(dtype=9), "unknown dtype"),
+        (dict(bt_it=3), "int32 or int64"),
+        (dict(scale=float("inf")), "scale must be finite"),
+        (dict(D=1024), "head_dim larger than 512"),
+    ]
+    for kw, msg in cases:
+        assert call(**kw) in (_native.MGI_EINVAL, _native.MGI_EUNSUPPORTED), kw
+        assert msg in lib.mgi_last_error().decode(), (kw, lib.mgi_last_error())
+
+
 def test_kv_append_rejects_bad_arguments_on_host():
     lib = _native.lib()
     st3, st5 = _i64(1, 1, 1), _i64(1, 1, 1, 1, 1)

@@ -1,0 +1,253 @@
+"""Parity of the HIP paged prefill attention (mgi_paged_prefill) on the MI355X.
+
+Kernel level: every element against the prefill oracle, evaluated in double
+on the same inputs. Tolerances are those of the reference's prefix test
+(tests/test_prefill_prefix_sdpa_v2.py:58-63) for fp32 -- atol 2e-5, rtol 2e-4
+-- and 2e-2 for bf16. Pools hold NaN in every slot no chunk row may see,
+tables are scattered permutations, and q is a strided view of a fused QKV
+row as in the model. Shapes cover the matrix-core buckets (head_dim 32, 64,
+128, 256), partial tiles, chunks after a long prefix, block sizes that are
+not powers of two, and the generic path (f16, head dims off the 16-byte
+grid, non-unit head-dim strides).
+
+Model level: the reference's prefix test recast for the "hip" prefill mode,
+the golden Mini-GPT token streams with HIP prefill and decode, and a bf16
+preemption runtime against the sdpa_v2 prefill.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import _e2e
+import _fixtures as fx
+from minivllm import hip_paged_decode as hpd
+from minivllm.block_manager import BlockManager
+from minivllm.kv_block_pool import KVBlockPool
+from minivllm.model import MiniGPT
+from minivllm.model_runner import ModelRunner
+from minivllm.sequence import SequenceState
+from oracle import paged_decode as ora
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+F32_TOL = dict(rtol=2e-4, atol=2e-5)
+BF16_TOL = dict(rtol=2e-2, atol=2e-2)
+
+
+def prefill_case(start, T, H, D, S, dtype, seed=0, L=2, layer=1, spare=3):
+    """Pool with positions 0..start+T-1 of one sequence written through a
+    scattered table and NaN elsewhere; q [T, H, D] a strided view."""
+    total = start + T
+    n_used = -(-total // S)
+    N = 2 * n_used + spare
+    g = torch.Generator().manual_seed(seed)
+    table = torch.randperm(N, generator=g)[:n_used]
+    k = torch.full((L, N, S, H, D), float("nan"))
+    v = torch.full((L, N, S, H, D), float("nan"))
+    pos = torch.arange(total)
+    k[layer, table[pos // S], pos % S] = torch.randn((total, H, D), generator=g)
+    v[layer, table[pos // S], pos % S] = torch.randn((total, H, D), generator=g)
+    pool = KVBlockPool(L, N, S, H, D, device=DEV, dtype=dtype)
+    pool.k.copy_(k.to(dtype))
+    pool.v.copy_(v.to(dtype))
+    qkv = torch.randn((T, 3, H, D), generator=g).to(dtype)
+    return qkv, pool, table, layer
+
+
+def run_hip(q, pool, table, start, layer):
+    print(f"  hip prefill start={start} T={q.shape[0]} H={q.shape[1]} D={q.shape[2]} "
+          f"S={pool.block_size} dtype={q.dtype} table={table.dtype}", flush=True)
+    with torch.inference_mode():
+        out = hpd.paged_prefill_hip(q, pool, table.to(DEV), start, layer)
+    torch.cuda.synchronize()
+    assert out.dtype == q.dtype and tuple(out.shape) == tuple(q.shape)
+    return out
+
+
+def check(out, q, pool, table, start, layer):
+    want = ora.paged_prefill(fx.to_numpy(q), fx.to_numpy(pool.k), fx.to_numpy(pool.v),
+                             table.numpy(), start, layer)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    tol = F32_TOL if q.dtype == torch.float32 else BF16_TOL
+    np.testing.assert_allclose(got, want, **tol)
+
+
+CASES = [
+    # start, T, H, D, S
+    (0, 1, 4, 128, 16),
+    (0, 7, 4, 128, 16),
+    (5, 7, 4, 128, 16),
+    (63, 65, 4, 128, 16),
+    (0, 406, 16, 128, 16),
+    (1000, 200, 16, 128, 16),
+    (0, 128, 8, 32, 16),
+    (100, 64, 8, 64, 16),
+    (30, 33, 2, 256, 16),
+    (20, 11, 4, 8, 4),
+    (17, 40, 3, 24, 5),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("start,T,H,D,S", CASES)
+def test_matches_oracle(start, T, H, D, S, dtype):
+    qkv, pool, table, layer = prefill_case(start, T, H, D, S, dtype)
+    q = qkv.to(DEV)[:, 0]
+    out = run_hip(q, pool, table, start, layer)
+    check(out, q, pool, table, start, layer)
+
+
+def test_int32_table_and_contiguous_q_match_int64_and_view():
+    qkv, pool, table, layer = prefill_case(37, 50, 4, 128, 16, torch.bfloat16, seed=3)
+    q = qkv.to(DEV)[:, 0]
+    a = run_hip(q, pool, table, 37, layer)
+    b = run_hip(q.contiguous(), pool, table.to(torch.int32), 37, layer)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype,D,strided", [(torch.float16, 64, False), (torch.bfloat16, 12, False),
+                                             (torch.float32, 64, True)],
+                         ids=["f16", "bf16_d12", "f32_dstride2"])
+def test_generic_path(dtype, D, strided):
+    start, T, H, S = 21, 30, 3, 16
+    qkv, pool, table, layer = prefill_case(start, T, H, D, S, dtype, seed=5)
+    q = qkv.to(DEV)[:, 0]
+    if strided:
+        q = torch.randn((T, H, 2 * D), generator=torch.Generator().manual_seed(9)).to(DEV)[..., ::2]
+    out = run_hip(q, pool, table, start, layer)
+    want = ora.paged_prefill(fx.to_numpy(q.float()), fx.to_numpy(pool.k.float()),
+                             fx.to_numpy(pool.v.float()), table.numpy(), start, layer)
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    np.testing.assert_allclose(out.float().cpu().numpy(), want, **tol)
+
+
+def test_one_row_chunk_equals_the_decode_kernel():
+    qkv, pool, table, layer = prefill_case(299, 1, 8, 128, 16, torch.float32, seed=7)
+    q = qkv.to(DEV)[:, 0]
+    pre = run_hip(q, pool, table, 299, layer)
+    with torch.inference_mode():
+        dec = hpd.paged_attention_batch_hip(q, pool, table[None].to(DEV),
+                                            torch.tensor([300], device=DEV), layer)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(pre, dec, rtol=2e-6, atol=2e-6)
+
+
+def test_validation_errors():
+    qkv, pool, table, layer = prefill_case(16, 16, 2, 64, 16, torch.float32)
+    q = qkv.to(DEV)[:, 0]
+    with pytest.raises(ValueError, match="shorter"):
+        hpd.paged_prefill_hip(q, pool, table[:1].to(DEV), 16, layer)
+    with pytest.raises(ValueError, match="GPU"):
+        hpd.paged_prefill_hip(q.cpu(), pool, table.to(DEV), 16, layer)
+    with pytest.raises(ValueError, match="dtype"):
+        hpd.paged_prefill_hip(q.to(torch.bfloat16), pool, table.to(DEV), 16, layer)
+    with pytest.raises(ValueError, match="layer_idx"):
+        hpd.paged_prefill_hip(q, pool, table.to(DEV), 16, 5)
+
+
+# ------------------------------------------------------------ model level
+
+def run_chunks(model, pieces, mode, block_size=4):
+    """tests/test_prefill_prefix_sdpa_v2.py:13-38 on the GPU: chunked prefill
+    of one prompt with an interleaved physical allocation and a NaN pool."""
+    model.set_prefill_fastpath_mode(mode)
+    n_blocks = 64
+    bm = BlockManager(n_blocks, block_size)
+    perm = list(range(n_blocks))[::2] + list(range(n_blocks))[1::2]
+    bm.free_blocks = list(reversed(perm))
+    attn = model.blocks[0].attn
+    pool = KVBlockPool(model.n_layer, n_blocks, block_size, attn.n_head, attn.head_size, device=DEV)
+    pool.k.fill_(float("nan"))
+    pool.v.fill_(float("nan"))
+    runner = ModelRunner(model, pool, bm)
+    prompt = [1 + i * 7 % (model.vocab_size - 1) for i in range(sum(pieces))]
+    seq = SequenceState(seq_id="seq", prompt_tokens=prompt, max_tokens=len(prompt) + 3)
+    outputs = []
+    with torch.inference_mode():
+        for length in pieces:
+            outputs.append(runner.prefill_chunk(seq, seq.prompt_pos, length).clone())
+            seq.prompt_pos += length
+    bm.check_invariants([seq])
+    k, v = pool.gather_sequence(seq)
+    return torch.cat(outputs, dim=1), k, v, list(seq.block_table)
+
+
+@pytest.fixture(scope="module")
+def prefix_model():
+    torch.manual_seed(2026)
+    m = MiniGPT(n_embd=32, n_head=4, vocab_size=64, block_size=192, dropout=0.0, n_layer=2)
+    return m.eval().to(DEV)
+
+
+@pytest.mark.parametrize("pieces", [[5, 7, 19], [1, 1, 9], [16, 1, 15], [8, 8, 8, 8],
+                                    [3, 5, 4, 16, 11], [16, 16, 16, 16], [64, 32, 32]],
+                         ids=lambda p: "-".join(map(str, p)))
+def test_reference_prefix_cases_with_hip_prefill(prefix_model, pieces):
+    print(f"  prefix case {pieces}", flush=True)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = run_chunks(prefix_model, pieces, "reference")
+    got = run_chunks(prefix_model, pieces, "hip")
+    assert got[3] == ref[3]
+    for a, b in zip(got[:3], ref[:3]):
+        torch.testing.assert_close(a, b, **F32_TOL)
+    assert torch.equal(got[0].argmax(-1), ref[0].argmax(-1))
+
+
+@pytest.mark.parametrize("case", _e2e.GOLDEN_C1["cases"], ids=lambda c: f"B{c['batch']}_P{c['prompt_len']}")
+def test_golden_tokens_with_hip_prefill_and_decode(case):
+    torch.backends.cuda.matmul.allow_tf32 = False
+    print(f"  C1 hip prefill + decode B{case['batch']}_P{case['prompt_len']}", flush=True)
+    tokens, rt = _e2e.run_c1(case, "cuda", "hip", prefill_mode="hip")
+    assert tokens == case["outputs"]
+    assert rt.iteration == case["iterations"]
+
+
+def test_bf16_runtime_hip_prefill_matches_sdpa_v2():
+    """bf16 preemption runtime, HIP decode, prefill 'hip' vs 'sdpa_v2': the
+    schedule is identical and token streams may differ only where the sdpa_v2
+    run's top-2 logit margin at the first divergence is a near tie (< 0.1)."""
+    spec = _e2e.RuntimeSpec(n_requests=12, prompt_mean=96, prompt_cap=320, output_len=12, n_embd=512,
+                            n_head=4, n_layer=2, vocab=2048, max_running=12, token_budget=256, seed=3)
+    prompts = _e2e.make_prompts(spec)
+    model = _e2e.make_model(spec, DEV, torch.bfloat16)
+    model.set_decode_attention_backend("hip")
+    out, margins = {}, {}
+    for mode in ("sdpa_v2", "hip"):
+        model.set_prefill_fastpath_mode(mode)
+        rt, seqs = _e2e.make_runtime(spec, model, prompts, DEV, torch.bfloat16)
+        if mode == "sdpa_v2":
+            inner_dec, inner_pre = rt.runner.decode_batch, rt.runner.prefill_chunk
+
+            def dec(sequences, inner=inner_dec):
+                pos = [s.length for s in sequences]
+                logits, toks = inner(sequences)
+                top = torch.topk(logits.float(), 2, dim=-1).values
+                for s, p, t in zip(sequences, pos, top.tolist()):
+                    margins[(s.seq_id, p)] = t[0] - t[1]
+                return logits, toks
+
+            def pre(seq, start_pos, num_tokens, inner=inner_pre):
+                logits = inner(seq=seq, start_pos=start_pos, num_tokens=num_tokens)
+                t = torch.topk(logits[0, -1].float(), 2).values.tolist()
+                margins[(seq.seq_id, start_pos + num_tokens - 1)] = t[0] - t[1]
+                return logits
+
+            rt.runner.decode_batch, rt.runner.prefill_chunk = dec, pre
+        stats = _e2e.run_to_completion(rt, seqs)
+        out[mode] = ({s.seq_id: (len(s.prompt_tokens), s.generated_tokens) for s in seqs}, stats)
+    assert out["sdpa_v2"][1]["preemptions"] > 0
+    for key in ("steps", "preemptions", "repeated_kv_tokens", "output_tokens"):
+        assert out["sdpa_v2"][1][key] == out["hip"][1][key], key
+    diverged = []
+    for sid, (plen, a) in out["sdpa_v2"][0].items():
+        b = out["hip"][0][sid][1]
+        if a != b:
+            k = next(i for i, (x, y) in enumerate(zip(a, b)) if x != y)
+            diverged.append((sid, k, margins[(sid, plen + k - 1)]))
+    print(f"  hip prefill vs sdpa_v2, bf16: diverged {diverged}", flush=True)
+    assert all(m < 0.1 for _, _, m in diverged), diverged
