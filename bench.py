@@ -51,6 +51,8 @@ def parse_args():
                          "vocab 32000, bf16, 256 requests, 128 output tokens) with the HIP backend and "
                          "report decode tokens/s")
     ap.add_argument("--e2e-requests", type=int, default=256)
+    ap.add_argument("--prefill", action="store_true",
+                    help="also time the paged prefill kernel (implied unless --no-extras)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run a device-to-device copy of this many MiB (3 times) so rocprof "
                          "counters can be scaled by a kernel of known traffic")
@@ -124,7 +126,8 @@ def copy_line(mib: int, dev, reps: int = 3):
     return {"mib": mib, "ms": round(ms, 4), "gbps_read_plus_write": round(2 * src.numel() / (ms * 1e-3) / 1e9, 1)}
 
 
-def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2"):
+def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2",
+             record_margins: bool = False):
     """The full runtime under recompute preemption with the HIP decode backend
     and the given prefill mode; with `graphs`, decode steps replay HIP graphs
     captured (before timing) for every batch bucket up to max_running."""
@@ -142,6 +145,7 @@ def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2"):
     _e2e.run_to_completion(rt, seqs)
     del rt, seqs
     rt, seqs = _e2e.make_runtime(spec, model, prompts, dev, torch.bfloat16)
+    margins = _e2e.record_margins(rt) if record_margins else None
     if graphs:
         rt.runner.enable_decode_graphs()
         rt.runner.capture_decode_graphs([b for b in (1, 2, 4, 8, 16, 32, 64, 128, 256) if b <= spec.max_running])
@@ -160,6 +164,9 @@ def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2"):
                   "prefill_mode": prefill_mode,
                   "decode_backend": "hip", "decode_graphs": graphs,
                   "tokens": [s.generated_tokens for s in seqs]})
+    if margins is not None:
+        stats.update({"margins": margins, "prompt_lens": [len(s.prompt_tokens) for s in seqs],
+                      "seq_ids": [s.seq_id for s in seqs]})
     return stats
 
 
@@ -199,6 +206,61 @@ def prefill_line(dev, start: int, T: int, H: int = 16, D: int = 128, steps: int 
     return {"start": start, "T": T, "H": H, "D": D, "us": round(hip_ms * 1e3, 2),
             "tflops": round(tflops, 1), "pct_of_bf16_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
             "sdpa_v2_fp32_us": round(sdpa_ms * 1e3, 1), "speedup_vs_sdpa_v2": round(sdpa_ms / hip_ms, 1)}
+
+
+def decode_step_latency(dev, batches=(1, 4, 16, 64, 256), ctx: int = 512, steps: int = 20):
+    """Wall time of one greedy decode step of the end-to-end model (dim 2048,
+    16 heads, 12 layers, vocab 32000, bf16, HIP decode) at batch B and context
+    `ctx`, including metadata packing, the host-to-device copy and the token
+    read-back: eager launches against the replay of the step captured for
+    B's bucket (table width fixed at the model's position limit)."""
+    import torch
+
+    import _e2e
+    from minivllm.decode_graphs import DecodeGraphs, metadata_views, pack_decode_metadata
+    from minivllm.kv_block_pool import KVBlockPool
+
+    spec = _e2e.RuntimeSpec()
+    model = _e2e.make_model(spec, dev, torch.bfloat16)
+    model.set_decode_attention_backend("hip")
+    S = spec.block_size
+    per_seq = -(-(ctx + 1) // S)
+    pool = KVBlockPool(spec.n_layer, max(batches) * per_seq, S, spec.n_head, spec.n_embd // spec.n_head,
+                       device=dev, dtype=torch.bfloat16)
+    pool.k.normal_()
+    pool.v.normal_()
+    M_graph = -(-model.block_size // S)
+    graphs = DecodeGraphs(model, pool, M_graph, buckets=tuple(batches))
+    out = {}
+    for B in batches:
+        tables = [list(range(b * per_seq, (b + 1) * per_seq)) for b in range(B)]
+        tokens = [(7 * b + 3) % spec.vocab for b in range(B)]
+        positions = [ctx] * B
+        slots = [t[ctx // S] * S + ctx % S for t in tables]
+
+        def eager():
+            buf = pack_decode_metadata(tokens, positions, slots, tables, B, per_seq).to(dev)
+            ids, meta = metadata_views(buf, B, per_seq)
+            logits = model.decode_batch(ids, meta, pool)[:, -1, :]
+            return torch.argmax(logits, dim=-1).tolist()
+
+        def replay():
+            return graphs.run(tokens, positions, slots, tables)[1]
+
+        graphs.capture(B)
+        res = {}
+        for name, fn in (("eager", eager), ("graph", replay)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            res[name] = (time.perf_counter() - t0) / steps * 1e3
+        out[f"B{B}"] = {"eager_ms": round(res["eager"], 3), "graph_ms": round(res["graph"], 3),
+                        "speedup": round(res["eager"] / res["graph"], 2)}
+        log(f"decode step latency B={B} ctx={ctx}: {out[f'B{B}']}")
+    return {"ctx": ctx, "by_batch": out}
 
 
 def attention_speedup_grid(dev):
@@ -363,7 +425,7 @@ def main() -> None:
             log(f"extra e2e speedup: {extras['e2e_small_model_speedup']}")
             torch.cuda.empty_cache()
 
-        if not args.no_extras or args.e2e:
+        if not args.no_extras or args.e2e or args.prefill:
             for start, T in ((0, 512), (2048, 2048)):
                 key = f"prefill_bf16_start{start}_T{T}_H16_D128"
                 extras[key] = prefill_line(dev, start, T)
@@ -378,13 +440,27 @@ def main() -> None:
                 log(f"end-to-end runtime, {args.e2e_requests} requests, prefill {mode}, decode graphs {graphs}")
                 extras[key] = e2e_line(args.e2e_requests, dev, graphs, mode)
                 torch.cuda.empty_cache()
+            log("e2e: untimed replay of the first configuration recording top-2 logit margins")
+            margins_run = e2e_line(args.e2e_requests, dev, False, "sdpa_v2", record_margins=True)
             base = extras[runs[0][0]]["tokens"]
+            extras[runs[0][0]]["deterministic_rerun"] = margins_run["tokens"] == base
             for key, _, _ in runs[1:]:
-                same = sum(a == b for a, b in zip(base, extras[key]["tokens"]))
+                other = extras[key]["tokens"]
+                same = sum(a == b for a, b in zip(base, other))
+                margin_at = []
+                for a, b, plen, sid in zip(base, other, margins_run["prompt_lens"], margins_run["seq_ids"]):
+                    if a != b:
+                        k = next(i for i, (x, y) in enumerate(zip(a, b)) if x != y)
+                        margin_at.append(margins_run["margins"].get((sid, plen + k - 1)))
+                known = [m for m in margin_at if m is not None]
                 extras[key]["identical_token_streams_vs_first"] = f"{same}/{args.e2e_requests}"
+                extras[key]["first_divergence_margin_max"] = round(max(known), 4) if known else None
+                extras[key]["first_divergences_at_exact_bf16_tie"] = sum(m == 0.0 for m in known)
             for key, _, _ in runs:
                 extras[key].pop("tokens")
                 log(f"e2e {key}: {extras[key]}")
+            extras["decode_step_latency_eager_vs_graph"] = decode_step_latency(dev)
+            torch.cuda.empty_cache()
 
         if args.calibrate_copy_mib:
             extras["copy_calibration"] = copy_line(args.calibrate_copy_mib, dev, reps=3)

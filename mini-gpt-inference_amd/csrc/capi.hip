@@ -351,6 +351,8 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
     return fail(MGI_EINVAL, "strides must be non-negative");
   if (start_pos + T >= (int64_t(1) << 31)) return fail(MGI_EUNSUPPORTED, "start_pos + T must be < 2^31");
   if (H > kMaxGridYZ) return fail(MGI_EUNSUPPORTED, "more than 65535 heads");
+  if (((T + 31) / 32) * H > (int64_t(1) << 24))
+    return fail(MGI_EUNSUPPORTED, "chunk rows x heads too large for one launch");
   if (D > 512) return fail(MGI_EUNSUPPORTED, "head_dim larger than 512");
 
   const int64_t eb = dtype_bytes(dtype);
@@ -399,10 +401,17 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
     a.s_shift = (S & (S - 1)) == 0 ? __builtin_ctzll((unsigned long long)S) : -1;
     a.N = N;
     a.scale_log2 = scale * 1.4426950408889634f;
-    // Four wavefronts (64 query rows) per workgroup once that still fills
-    // the chip; two otherwise.
-    const int waves = ((T + 63) / 64) * H >= device_cus() ? 4 : 2;
-    e = launch_paged_prefill(a, bf16, dp, waves, st);
+    // Largest workgroup that still gives every compute unit one: four
+    // wavefronts of two 16-row query blocks (bf16), four of one, or two of one.
+    const int64_t cus = device_cus();
+    int waves = 2, qpw = 1;
+    if (bf16 && ((T + 127) / 128) * H >= cus) {
+      waves = 4;
+      qpw = 2;
+    } else if (((T + 63) / 64) * H >= cus) {
+      waves = 4;
+    }
+    e = launch_paged_prefill(a, bf16, dp, waves, qpw, st);
   } else {
     // Any other shape: the chunk as T single-query rows of the generic decode
     // kernel, sharing one table row, with context lengths start_pos + t + 1.

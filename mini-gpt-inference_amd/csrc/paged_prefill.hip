@@ -8,11 +8,13 @@
 // (minivllm/attention.py:269-299, paged_attention_online) and with the
 // gathered-prefix SDPA of mode sdpa_v2 (minivllm/attention.py:229-267).
 //
-// Work split: one workgroup per (query tile, head); each wavefront owns 16
-// query rows. Keys stream through LDS in tiles of 64: K row-major, V
-// transposed. Each wave computes S^T = K Q^T and O^T += V^T P^T with
-// 16x16 MFMA tiles, so a lane's accumulator column is one query row: the
-// online-softmax state (max, sum) is per lane and P needs no transpose.
+// Work split: one workgroup per (query tile, head); each wavefront owns one
+// or two blocks of 16 query rows. Keys stream through LDS in tiles of 64 (K
+// row-major, V transposed, two stages so one barrier per tile suffices).
+// Each wave computes S^T = K Q^T and O^T += V^T P^T with 16x16 MFMA tiles,
+// so a lane's accumulator column is one query row: the online-softmax state
+// (max, sum) is per lane and P needs no transpose. With two query blocks per
+// wave every K and V fragment read from LDS feeds two MFMAs.
 //
 // Numerics: fp32 accumulation and softmax in the log2 domain; bf16 inputs
 // use v_mfma_f32_16x16x32_bf16 with P rounded to bf16 for the PV product,
@@ -52,10 +54,13 @@ __device__ __forceinline__ float cross_group_sum(float x) {
   return x + shfl_xor32(x);
 }
 
-// Block-table slot of key `key` of the workgroup: (physical block, offset),
-// or (-1, 0) for keys past the chunk or invalid table entries.
-__device__ __forceinline__ int2 key_slot(const PrefillArgs& a, int key, int kv_end) {
-  if (key >= kv_end) return make_int2(-1, 0);
+// Element offsets of key `key`'s K and V rows (relative to the head's base
+// in the layer), or -1 for keys past the chunk or invalid table entries.
+struct KeyRows {
+  int64_t k, v;
+};
+__device__ __forceinline__ KeyRows key_rows(const PrefillArgs& a, int key, int kv_end) {
+  if (key >= kv_end) return KeyRows{-1, -1};
   int blk, off;
   if (a.s_shift >= 0) {
     blk = key >> a.s_shift;
@@ -65,11 +70,32 @@ __device__ __forceinline__ int2 key_slot(const PrefillArgs& a, int key, int kv_e
     off = key - blk * a.S;
   }
   const int64_t phys = load_index(a.bt, a.bt_i64, (int64_t)blk * a.bt_s);
-  if (phys < 0 || phys >= a.N) return make_int2(-1, 0);
-  return make_int2((int)phys, off);
+  if (phys < 0 || phys >= a.N) return KeyRows{-1, -1};
+  return KeyRows{phys * a.k_sn + off * a.k_ss, phys * a.v_sn + off * a.v_ss};
 }
 
-template <typename T, int DP, int WAVES>
+// Online-softmax reference maxima move only when a tile's maximum exceeds
+// them by more than this (log2 units), so exponentials stay <= 2^8 and the
+// accumulators are rescaled on few tiles.
+constexpr float kRescaleSlack = 8.f;
+
+// Two bf16 values -> packed bf16x2 (hardware round to nearest even).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Column of key k (0..63) in a bf16 V^T tile row. Keys 32c + 16h + 4g + i
+// sit at 32c + 8g + 4h + i, so the eight keys one lane feeds to a PV MFMA
+// (4g+i and 16+4g+i of a 32-key slice) are one 16-byte LDS read.
+__device__ __forceinline__ int vt_col_bf16(int k) {
+  return (k & 32) | ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3);
+}
+
+// T: element type; DP: head dim padded to the MFMA K width (D <= DP);
+// WAVES: wavefronts per workgroup; QPW: 16-row query blocks per wavefront.
+template <typename T, int DP, int WAVES, int QPW>
 __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillArgs a) {
   using E = PF<T>;
   constexpr int CH = E::kChunk;
@@ -79,37 +105,59 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   constexpr int NT = 64 * WAVES;
   constexpr int ITEMS = 16 * CPR;              // (4-key group, chunk) pairs per tile
   constexpr int IPT = (ITEMS + NT - 1) / NT;
-  constexpr int QB = 16 * WAVES;               // query rows per workgroup
+  constexpr int QB = 16 * QPW * WAVES;         // query rows per workgroup
   constexpr bool kBF16 = sizeof(T) == 2;
   constexpr int NQF = kBF16 ? DP / 32 : DP / 16;   // Q fragments (16 bytes each)
   constexpr int NDB = DP / 16;                     // 16-wide head-dim blocks of O^T
 
-  __shared__ __align__(16) T k_lds[kTileKeys * KROW];
-  __shared__ __align__(16) T vt_lds[DP * VROW];
-  __shared__ int2 slots[2][kTileKeys];
+  // Two stages: tile t is read from one while tile t+1 is written to the other.
+  __shared__ __align__(16) T k_lds[2][kTileKeys * KROW];
+  __shared__ __align__(16) T vt_lds[2][DP * VROW];
+  __shared__ KeyRows slots[2][kTileKeys];
 
-  const int qt = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest query tiles first
-  const int h = blockIdx.y;
+  // 1-D grid of nq * H workgroups, dispatched round-robin over the XCDs
+  // (workgroup id mod 8). With H a multiple of 8, every query tile of head h
+  // runs on XCD h mod 8, so each XCD's L2 holds the K/V of H/8 heads only.
+  // Within a head, the longest (latest) query tiles go first.
+  const int nq = (a.T + QB - 1) / QB;
+  const int wg = (int)blockIdx.x;
+  int h, qr;
+  if ((a.H & 7) == 0) {
+    const int j = wg >> 3;
+    h = (wg & 7) + 8 * (j / nq);
+    qr = j % nq;
+  } else {
+    h = wg / nq;
+    qr = wg % nq;
+  }
+  const int qt = nq - 1 - qr;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
-  const int qw0 = qt * QB + wave * 16;
-  const int qi = qw0 + col;
-  const bool q_ok = qi < a.T;
-  const int qpos = a.start + (q_ok ? qi : a.T - 1);
+  const int qw0 = qt * QB + wave * 16 * QPW;
   const int kv_end = a.start + min(a.T, (qt + 1) * QB);
   const bool wave_active = qw0 < a.T;
-  const int wave_last = a.start + min(a.T, qw0 + 16) - 1;
+  const int wave_first = a.start + qw0;
+  const int wave_last = a.start + min(a.T, qw0 + 16 * QPW) - 1;
   const int ntiles = (kv_end + kTileKeys - 1) / kTileKeys;
 
+  int qi[QPW], qpos[QPW];
+#pragma unroll
+  for (int b = 0; b < QPW; ++b) {
+    qi[b] = qw0 + 16 * b + col;
+    qpos[b] = a.start + (qi[b] < a.T ? qi[b] : a.T - 1);
+  }
+
   // ---- this lane's query fragments (zero past the chunk or past D)
-  uint4 qf[NQF];
-  {
-    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)(q_ok ? qi : 0) * a.q_st +
+  uint4 qf[QPW][NQF];
+#pragma unroll
+  for (int b = 0; b < QPW; ++b) {
+    const bool ok = qi[b] < a.T;
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)(ok ? qi[b] : 0) * a.q_st +
                     (int64_t)h * a.q_sh;
 #pragma unroll
     for (int f = 0; f < NQF; ++f) {
       const int d = kBF16 ? 32 * f + 8 * g : 16 * f + 4 * g;
-      qf[f] = (q_ok && d < a.D) ? *reinterpret_cast<const uint4*>(qrow + d) : make_uint4(0, 0, 0, 0);
+      qf[b][f] = (ok && d < a.D) ? *reinterpret_cast<const uint4*>(qrow + d) : make_uint4(0, 0, 0, 0);
     }
   }
 
@@ -119,7 +167,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   // Staging registers: item j of this thread covers 4 keys x one chunk, for K
   // (keys vary slowest: lanes sweep the head dim) and V (lanes sweep keys).
   uint4 kr[IPT][4], vr[IPT][4];
-  auto load_tile = [&](int buf) {
+  auto load_tile = [&](int sb) {
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
       const int it = tid + NT * j;
@@ -128,20 +176,18 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
       const int kq_v = it % 16, dc_v = it / 16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int2 sk = slots[buf][4 * kq_k + r];
-        const int2 sv = slots[buf][4 * kq_v + r];
-        const bool okk = in && sk.x >= 0 && dc_k * CH < a.D;
-        const bool okv = in && sv.x >= 0 && dc_v * CH < a.D;
-        kr[j][r] = okk ? *reinterpret_cast<const uint4*>(kb_ + (int64_t)sk.x * a.k_sn +
-                                                         (int64_t)sk.y * a.k_ss + dc_k * CH)
-                       : make_uint4(0, 0, 0, 0);
-        vr[j][r] = okv ? *reinterpret_cast<const uint4*>(vb_ + (int64_t)sv.x * a.v_sn +
-                                                         (int64_t)sv.y * a.v_ss + dc_v * CH)
-                       : make_uint4(0, 0, 0, 0);
+        const int64_t ko = slots[sb][4 * kq_k + r].k;
+        const int64_t vo = slots[sb][4 * kq_v + r].v;
+        const bool okk = in && ko >= 0 && dc_k * CH < a.D;
+        const bool okv = in && vo >= 0 && dc_v * CH < a.D;
+        kr[j][r] = okk ? *reinterpret_cast<const uint4*>(kb_ + ko + dc_k * CH) : make_uint4(0, 0, 0, 0);
+        vr[j][r] = okv ? *reinterpret_cast<const uint4*>(vb_ + vo + dc_v * CH) : make_uint4(0, 0, 0, 0);
       }
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
+    T* kl = k_lds[buf];
+    T* vl = vt_lds[buf];
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
       const int it = tid + NT * j;
@@ -150,9 +196,10 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
       const int kq_v = it % 16, dc_v = it / 16;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<uint4*>(&k_lds[(4 * kq_k + r) * KROW + dc_k * CH]) = kr[j][r];
+        *reinterpret_cast<uint4*>(&kl[(4 * kq_k + r) * KROW + dc_k * CH]) = kr[j][r];
       if constexpr (kBF16) {
-        // 8 head dims x 4 keys -> eight 4-key rows of V^T.
+        // 8 head dims x 4 keys -> eight 4-key runs of V^T rows.
+        const int vc = vt_col_bf16(4 * kq_v);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int w = e >> 1, sh = (e & 1) * 16;
@@ -163,165 +210,211 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
           uint2 pk;
           pk.x = word(vr[j][0]) | (word(vr[j][1]) << 16);
           pk.y = word(vr[j][2]) | (word(vr[j][3]) << 16);
-          *reinterpret_cast<uint2*>(&vt_lds[(8 * dc_v + e) * VROW + 4 * kq_v]) = pk;
+          *reinterpret_cast<uint2*>(&vl[(8 * dc_v + e) * VROW + vc]) = pk;
         }
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           auto word = [&](const uint4& x) { return e == 0 ? x.x : e == 1 ? x.y : e == 2 ? x.z : x.w; };
           uint4 pk = make_uint4(word(vr[j][0]), word(vr[j][1]), word(vr[j][2]), word(vr[j][3]));
-          *reinterpret_cast<uint4*>(&vt_lds[(4 * dc_v + e) * VROW + 4 * kq_v]) = pk;
+          *reinterpret_cast<uint4*>(&vl[(4 * dc_v + e) * VROW + 4 * kq_v]) = pk;
         }
       }
     }
   };
 
-  f32x4_t oacc[NDB];
+  f32x4_t oacc[QPW][NDB];
+  float m_run[QPW], l_part[QPW];
 #pragma unroll
-  for (int i = 0; i < NDB; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_part = 0.f;
-
-  // Prologue: slots of tile 0 (and a prefetch of tile 1), then tile 0's data.
-  int2 slot_next = make_int2(-1, 0);
-  if (tid < kTileKeys) {
-    slots[0][tid] = key_slot(a, tid, kv_end);
-    if (ntiles > 1) slot_next = key_slot(a, kTileKeys + tid, kv_end);
+  for (int b = 0; b < QPW; ++b) {
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) oacc[b][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[b] = -INFINITY;
+    l_part[b] = 0.f;
   }
-  __syncthreads();
-  load_tile(0);
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int kt0 = t * kTileKeys;
-    if (tid < kTileKeys) {
-      slots[(t + 1) & 1][tid] = slot_next;
-      if (t + 2 < ntiles) slot_next = key_slot(a, (t + 2) * kTileKeys + tid, kv_end);
-    }
-    store_tile();
-    __syncthreads();
-    if (t + 1 < ntiles) load_tile((t + 1) & 1);
-
-    if (wave_active && kt0 <= wave_last) {
-      // ---- S^T tile: lane holds keys kt0 + 16*kb + 4*g + i of query column `col`
-      f32x4_t s[4];
+  auto compute = [&](int buf, int kt0) {
+    const T* kl = k_lds[buf];
+    const T* vl = vt_lds[buf];
+    // ---- S^T blocks: lane holds keys kt0 + 16*kb + 4*g + i of query column `col`
+    f32x4_t s[QPW][4];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        s[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        const T* krow = &k_lds[(16 * kb + col) * KROW];
+    for (int b = 0; b < QPW; ++b)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) s[b][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const T* krow = &kl[(16 * kb + col) * KROW];
+#pragma unroll
+      for (int f = 0; f < NQF; ++f) {
         if constexpr (kBF16) {
+          const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(krow + 32 * f + 8 * g));
 #pragma unroll
-          for (int f = 0; f < NQF; ++f) {
-            const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * f + 8 * g);
-            s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv),
-                                                            __builtin_bit_cast(bf16x8_t, qf[f]),
-                                                            s[kb], 0, 0, 0);
-          }
+          for (int b = 0; b < QPW; ++b)
+            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, __builtin_bit_cast(bf16x8_t, qf[b][f]),
+                                                               s[b][kb], 0, 0, 0);
         } else {
+          const float4 kv = *reinterpret_cast<const float4*>(krow + 16 * f + 4 * g);
 #pragma unroll
-          for (int f = 0; f < NQF; ++f) {
-            const float4 kv = *reinterpret_cast<const float4*>(krow + 16 * f + 4 * g);
-            const float4 qv = __builtin_bit_cast(float4, qf[f]);
-            s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qv.x, s[kb], 0, 0, 0);
-            s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qv.y, s[kb], 0, 0, 0);
-            s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qv.z, s[kb], 0, 0, 0);
-            s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qv.w, s[kb], 0, 0, 0);
+          for (int b = 0; b < QPW; ++b) {
+            const float4 qv = __builtin_bit_cast(float4, qf[b][f]);
+            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qv.x, s[b][kb], 0, 0, 0);
+            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qv.y, s[b][kb], 0, 0, 0);
+            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qv.z, s[b][kb], 0, 0, 0);
+            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qv.w, s[b][kb], 0, 0, 0);
           }
         }
       }
+    }
 
-      // ---- causal mask, online softmax (log2 domain, per query column)
-      float p[4][4];
+    // ---- causal mask (diagonal tiles only), online softmax per query column.
+    // Raw scores s; the log2-domain score is s * scale_log2 (scale > 0, so the
+    // maximum of raw scores gives the maximum of scaled ones).
+    const bool full = kt0 + kTileKeys - 1 <= wave_first;
+    const float c = a.scale_log2;
+    float p[QPW][4][4];
+#pragma unroll
+    for (int b = 0; b < QPW; ++b) {
       float mt = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kt0 + 16 * kb + 4 * g + i;
-          const float x = s[kb][i] * a.scale_log2;
-          p[kb][i] = key <= qpos ? x : -INFINITY;
-          mt = fmaxf(mt, p[kb][i]);
+          p[b][kb][i] = (full || kt0 + 16 * kb + 4 * g + i <= qpos[b]) ? s[b][kb][i] : -INFINITY;
+          mt = fmaxf(mt, p[b][kb][i]);
         }
-      mt = cross_group_max(mt);
-      const float m_new = fmaxf(m_run, mt);   // finite: key 0 is visible to every query
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
+      mt = cross_group_max(mt) * c;
+      // The reference maximum moves (and the state is rescaled) only when some
+      // column outgrows it by more than the slack; the first visited tile
+      // always sets it (key 0 is visible to every query, so it is finite).
+      if (__builtin_amdgcn_ballot_w64(mt > m_run[b] + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(m_run[b], mt);
+        const float alpha = fast_exp2(m_run[b] - m_new);
+        m_run[b] = m_new;
+        l_part[b] *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) oacc[b][db] *= alpha;
+      }
+      const float neg_m = -m_run[b];
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[kb][i] = fast_exp2(p[kb][i] - m_new);
-          ps += p[kb][i];
+          p[b][kb][i] = fast_exp2(fmaf(p[b][kb][i], c, neg_m));
+          ps += p[b][kb][i];
         }
-      l_part = l_part * alpha + ps;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) oacc[db] *= alpha;
+      l_part[b] += ps;
+    }
 
-      // ---- O^T += V^T P^T
-      if constexpr (kBF16) {
+    // ---- O^T += V^T P^T
+    if constexpr (kBF16) {
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          uint4 pb;
-          pb.x = (uint32_t)f32_to_bf16(p[2 * c][0]) | ((uint32_t)f32_to_bf16(p[2 * c][1]) << 16);
-          pb.y = (uint32_t)f32_to_bf16(p[2 * c][2]) | ((uint32_t)f32_to_bf16(p[2 * c][3]) << 16);
-          pb.z = (uint32_t)f32_to_bf16(p[2 * c + 1][0]) | ((uint32_t)f32_to_bf16(p[2 * c + 1][1]) << 16);
-          pb.w = (uint32_t)f32_to_bf16(p[2 * c + 1][2]) | ((uint32_t)f32_to_bf16(p[2 * c + 1][3]) << 16);
+      for (int c = 0; c < 2; ++c) {
+        bf16x8_t pb[QPW];
 #pragma unroll
-          for (int db = 0; db < NDB; ++db) {
-            const T* vrow = &vt_lds[(16 * db + col) * VROW + 32 * c + 4 * g];
-            const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
-            const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
-            const uint4 va = make_uint4(v0.x, v0.y, v1.x, v1.y);
-            oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va),
-                                                               __builtin_bit_cast(bf16x8_t, pb),
-                                                               oacc[db], 0, 0, 0);
+        for (int b = 0; b < QPW; ++b) {
+          const uint4 w = make_uint4(pack_bf16x2(p[b][2 * c][0], p[b][2 * c][1]),
+                                     pack_bf16x2(p[b][2 * c][2], p[b][2 * c][3]),
+                                     pack_bf16x2(p[b][2 * c + 1][0], p[b][2 * c + 1][1]),
+                                     pack_bf16x2(p[b][2 * c + 1][2], p[b][2 * c + 1][3]));
+          pb[b] = __builtin_bit_cast(bf16x8_t, w);
+        }
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const bf16x8_t va = __builtin_bit_cast(
+              bf16x8_t, *reinterpret_cast<const uint4*>(&vl[(16 * db + col) * VROW + 32 * c + 8 * g]));
+#pragma unroll
+          for (int b = 0; b < QPW; ++b)
+            oacc[b][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[b], oacc[b][db], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const float4 vv = *reinterpret_cast<const float4*>(&vl[(16 * db + col) * VROW + 16 * kb + 4 * g]);
+#pragma unroll
+          for (int b = 0; b < QPW; ++b) {
+            oacc[b][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, p[b][kb][0], oacc[b][db], 0, 0, 0);
+            oacc[b][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, p[b][kb][1], oacc[b][db], 0, 0, 0);
+            oacc[b][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, p[b][kb][2], oacc[b][db], 0, 0, 0);
+            oacc[b][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, p[b][kb][3], oacc[b][db], 0, 0, 0);
           }
         }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int db = 0; db < NDB; ++db) {
-            const float4 vv = *reinterpret_cast<const float4*>(
-                &vt_lds[(16 * db + col) * VROW + 16 * kb + 4 * g]);
-            oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, p[kb][0], oacc[db], 0, 0, 0);
-            oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, p[kb][1], oacc[db], 0, 0, 0);
-            oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, p[kb][2], oacc[db], 0, 0, 0);
-            oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, p[kb][3], oacc[db], 0, 0, 0);
-          }
+    }
+  };
+
+  // ---- pipeline: tile t+1 is in registers while tile t is computed; its
+  // block-table slots are in LDS two tiles ahead.
+  KeyRows slot_next{-1, -1};
+  if (tid < kTileKeys) {
+    slots[0][tid] = key_rows(a, tid, kv_end);
+    if (ntiles > 1) slot_next = key_rows(a, kTileKeys + tid, kv_end);
+  }
+  __syncthreads();
+  load_tile(0);
+  if (tid < kTileKeys) {
+    slots[1][tid] = slot_next;
+    if (ntiles > 2) slot_next = key_rows(a, 2 * kTileKeys + tid, kv_end);
+  }
+  store_tile(0);
+  __syncthreads();
+  if (ntiles > 1) load_tile(1);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int kt0 = t * kTileKeys;
+    if (wave_active && kt0 <= wave_last) compute(t & 1, kt0);
+    if (t + 1 < ntiles) {
+      if (tid < kTileKeys) {
+        slots[t & 1][tid] = slot_next;   // tile t+2
+        if (t + 3 < ntiles) slot_next = key_rows(a, (t + 3) * kTileKeys + tid, kv_end);
       }
+      store_tile((t + 1) & 1);
     }
     __syncthreads();
+    if (t + 2 < ntiles) load_tile(t & 1);
   }
 
   // ---- normalise and store: lane holds out[qi, h, 16*db + 4*g + 0..3]
-  const float l = cross_group_sum(l_part);
-  if (!q_ok) return;
-  const float inv = 1.f / l;
-  T* orow = reinterpret_cast<T*>(a.out) + (int64_t)qi * a.o_st + (int64_t)h * a.o_sh;
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    const int d0 = 16 * db + 4 * g;
-    if (d0 >= a.D) continue;
-    if constexpr (kBF16) {
-      uint2 w;
-      w.x = (uint32_t)f32_to_bf16(oacc[db][0] * inv) | ((uint32_t)f32_to_bf16(oacc[db][1] * inv) << 16);
-      w.y = (uint32_t)f32_to_bf16(oacc[db][2] * inv) | ((uint32_t)f32_to_bf16(oacc[db][3] * inv) << 16);
-      *reinterpret_cast<uint2*>(orow + d0) = w;
-    } else {
-      *reinterpret_cast<float4*>(orow + d0) =
-          make_float4(oacc[db][0] * inv, oacc[db][1] * inv, oacc[db][2] * inv, oacc[db][3] * inv);
+  for (int b = 0; b < QPW; ++b) {
+    const float l = cross_group_sum(l_part[b]);
+    if (qi[b] >= a.T) continue;
+    const float inv = 1.f / l;
+    T* orow = reinterpret_cast<T*>(a.out) + (int64_t)qi[b] * a.o_st + (int64_t)h * a.o_sh;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int d0 = 16 * db + 4 * g;
+      if (d0 >= a.D) continue;
+      if constexpr (kBF16) {
+        uint2 w;
+        w.x = pack_bf16x2(oacc[b][db][0] * inv, oacc[b][db][1] * inv);
+        w.y = pack_bf16x2(oacc[b][db][2] * inv, oacc[b][db][3] * inv);
+        *reinterpret_cast<uint2*>(orow + d0) = w;
+      } else {
+        *reinterpret_cast<float4*>(orow + d0) = make_float4(oacc[b][db][0] * inv, oacc[b][db][1] * inv,
+                                                            oacc[b][db][2] * inv, oacc[b][db][3] * inv);
+      }
     }
   }
 }
 
 template <typename T, int DP>
-hipError_t launch_dp(const PrefillArgs& a, int waves, hipStream_t stream) {
-  const int qb = 16 * waves;
-  const dim3 grid((unsigned)((a.T + qb - 1) / qb), (unsigned)a.H);
+hipError_t launch_dp(const PrefillArgs& a, int waves, int qpw, hipStream_t stream) {
+  const int qb = 16 * waves * qpw;
+  const dim3 grid((unsigned)(((int64_t)a.T + qb - 1) / qb * a.H));
+  if constexpr (sizeof(T) == 2) {
+    if (waves == 4 && qpw == 2) {
+      hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 4, 2>), grid, dim3(256), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
   if (waves == 4)
-    hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 4, 1>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 2>), grid, dim3(128), 0, stream, a);
+    hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 2, 1>), grid, dim3(128), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -335,20 +428,20 @@ int prefill_head_dim_bucket(int dtype_is_bf16, int D) {
   return 0;
 }
 
-hipError_t launch_paged_prefill(const PrefillArgs& a, bool bf16, int dp, int waves,
+hipError_t launch_paged_prefill(const PrefillArgs& a, bool bf16, int dp, int waves, int qpw,
                                 hipStream_t stream) {
   if (bf16) {
     switch (dp) {
-      case 32: return launch_dp<bf16_t, 32>(a, waves, stream);
-      case 64: return launch_dp<bf16_t, 64>(a, waves, stream);
-      case 128: return launch_dp<bf16_t, 128>(a, waves, stream);
-      case 256: return launch_dp<bf16_t, 256>(a, waves, stream);
+      case 32: return launch_dp<bf16_t, 32>(a, waves, qpw, stream);
+      case 64: return launch_dp<bf16_t, 64>(a, waves, qpw, stream);
+      case 128: return launch_dp<bf16_t, 128>(a, waves, qpw, stream);
+      case 256: return launch_dp<bf16_t, 256>(a, waves, qpw, stream);
     }
   } else {
     switch (dp) {
-      case 32: return launch_dp<float, 32>(a, waves, stream);
-      case 64: return launch_dp<float, 64>(a, waves, stream);
-      case 128: return launch_dp<float, 128>(a, waves, stream);
+      case 32: return launch_dp<float, 32>(a, waves, 1, stream);
+      case 64: return launch_dp<float, 64>(a, waves, 1, stream);
+      case 128: return launch_dp<float, 128>(a, waves, 1, stream);
     }
   }
   return hipErrorInvalidValue;

@@ -100,6 +100,45 @@ def make_runtime(spec: RuntimeSpec, model: MiniGPT, prompts, device, dtype):
     return rt, seqs
 
 
+def record_margins(rt: MiniRuntime) -> dict:
+    """Wraps the runner so every greedy choice records its top-2 logit
+    margin, keyed by (seq_id, position of the last input token): decode steps
+    at the sequence length before the step, prefill chunks at their last row.
+    Returns the (filling) dict."""
+    margins: dict = {}
+    inner_dec, inner_pre = rt.runner.decode_batch, rt.runner.prefill_chunk
+
+    def decode_batch(sequences):
+        pos = [s.length for s in sequences]
+        logits, toks = inner_dec(sequences)
+        top = torch.topk(logits.float(), 2, dim=-1).values.tolist()
+        for s, p, t in zip(sequences, pos, top):
+            margins[(s.seq_id, p)] = t[0] - t[1]
+        return logits, toks
+
+    def prefill_chunk(seq, start_pos, num_tokens):
+        logits = inner_pre(seq=seq, start_pos=start_pos, num_tokens=num_tokens)
+        t = torch.topk(logits[0, -1].float(), 2).values.tolist()
+        margins[(seq.seq_id, start_pos + num_tokens - 1)] = t[0] - t[1]
+        return logits
+
+    rt.runner.decode_batch, rt.runner.prefill_chunk = decode_batch, prefill_chunk
+    return margins
+
+
+def first_divergences(base: dict, other: dict, margins: dict) -> list:
+    """base/other: seq_id -> (prompt_len, generated tokens). For each stream
+    that differs: (seq_id, index of the first different token, the base run's
+    top-2 margin at that choice)."""
+    out = []
+    for sid, (plen, a) in base.items():
+        b = other[sid][1]
+        if a != b:
+            k = next(i for i, (x, y) in enumerate(zip(a, b)) if x != y)
+            out.append((sid, k, margins.get((sid, plen + k - 1))))
+    return out
+
+
 def run_to_completion(rt: MiniRuntime, seqs, max_steps: int = 100000, on_step=None) -> dict:
     """Steps the runtime until every request finished; returns throughput figures."""
     sync = torch.cuda.synchronize if torch.cuda.is_available() else (lambda: None)

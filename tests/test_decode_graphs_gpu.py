@@ -95,29 +95,14 @@ def test_preemption_runtime_graphs_match_eager(dtype):
         if graphs:
             rt.runner.enable_decode_graphs()
         else:
-            inner = rt.runner.decode_batch
-
-            def capture(sequences, inner=inner):
-                pos = [s.length for s in sequences]
-                logits, toks = inner(sequences)
-                top = torch.topk(logits.float(), 2, dim=-1).values
-                for s, p, v in zip(sequences, pos, top.tolist()):
-                    margins[(s.seq_id, p)] = v[0] - v[1]
-                return logits, toks
-
-            rt.runner.decode_batch = capture
+            margins = _e2e.record_margins(rt)
         stats = _e2e.run_to_completion(rt, seqs)
         out[graphs] = ({s.seq_id: (len(s.prompt_tokens), s.generated_tokens) for s in seqs}, stats)
     assert out[False][1]["preemptions"] > 0
     for key in ("steps", "preemptions", "repeated_kv_tokens", "output_tokens"):
         assert out[False][1][key] == out[True][1][key], key
-    diverged = []
-    for sid, (plen, a) in out[False][0].items():
-        b = out[True][0][sid][1]
-        if a != b:
-            k = next(i for i, (x, y) in enumerate(zip(a, b)) if x != y)
-            assert k > 0
-            diverged.append((sid, k, margins[(sid, plen + k - 1)]))
+    diverged = _e2e.first_divergences(out[False][0], out[True][0], margins)
+    assert all(k > 0 for _, k, _ in diverged)
     print(f"  graphs vs eager, {dtype}: diverged {diverged}", flush=True)
     if dtype == torch.float32:
         assert not diverged

@@ -221,33 +221,12 @@ def test_bf16_runtime_hip_prefill_matches_sdpa_v2():
         model.set_prefill_fastpath_mode(mode)
         rt, seqs = _e2e.make_runtime(spec, model, prompts, DEV, torch.bfloat16)
         if mode == "sdpa_v2":
-            inner_dec, inner_pre = rt.runner.decode_batch, rt.runner.prefill_chunk
-
-            def dec(sequences, inner=inner_dec):
-                pos = [s.length for s in sequences]
-                logits, toks = inner(sequences)
-                top = torch.topk(logits.float(), 2, dim=-1).values
-                for s, p, t in zip(sequences, pos, top.tolist()):
-                    margins[(s.seq_id, p)] = t[0] - t[1]
-                return logits, toks
-
-            def pre(seq, start_pos, num_tokens, inner=inner_pre):
-                logits = inner(seq=seq, start_pos=start_pos, num_tokens=num_tokens)
-                t = torch.topk(logits[0, -1].float(), 2).values.tolist()
-                margins[(seq.seq_id, start_pos + num_tokens - 1)] = t[0] - t[1]
-                return logits
-
-            rt.runner.decode_batch, rt.runner.prefill_chunk = dec, pre
+            margins = _e2e.record_margins(rt)
         stats = _e2e.run_to_completion(rt, seqs)
         out[mode] = ({s.seq_id: (len(s.prompt_tokens), s.generated_tokens) for s in seqs}, stats)
     assert out["sdpa_v2"][1]["preemptions"] > 0
     for key in ("steps", "preemptions", "repeated_kv_tokens", "output_tokens"):
         assert out["sdpa_v2"][1][key] == out["hip"][1][key], key
-    diverged = []
-    for sid, (plen, a) in out["sdpa_v2"][0].items():
-        b = out["hip"][0][sid][1]
-        if a != b:
-            k = next(i for i, (x, y) in enumerate(zip(a, b)) if x != y)
-            diverged.append((sid, k, margins[(sid, plen + k - 1)]))
+    diverged = _e2e.first_divergences(out["sdpa_v2"][0], out["hip"][0], margins)
     print(f"  hip prefill vs sdpa_v2, bf16: diverged {diverged}", flush=True)
     assert all(m < 0.1 for _, _, m in diverged), diverged
