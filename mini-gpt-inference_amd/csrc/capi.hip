@@ -401,17 +401,10 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
     a.s_shift = (S & (S - 1)) == 0 ? __builtin_ctzll((unsigned long long)S) : -1;
     a.N = N;
     a.scale_log2 = scale * 1.4426950408889634f;
-    // Largest workgroup that still gives every compute unit one: four
-    // wavefronts of two 16-row query blocks (bf16), four of one, or two of one.
-    const int64_t cus = device_cus();
-    int waves = 2, qpw = 1;
-    if (bf16 && ((T + 127) / 128) * H >= cus) {
-      waves = 4;
-      qpw = 2;
-    } else if (((T + 63) / 64) * H >= cus) {
-      waves = 4;
-    }
-    e = launch_paged_prefill(a, bf16, dp, waves, qpw, st);
+    // Four wavefronts of 16 query rows share each staged K/V tile; chunks of
+    // at most 32 rows use two.
+    const int waves = T <= 32 ? 2 : 4;
+    e = launch_paged_prefill(a, bf16, dp, waves, 1, st);
   } else {
     // Any other shape: the chunk as T single-query rows of the generic decode
     // kernel, sharing one table row, with context lengths start_pos + t + 1.

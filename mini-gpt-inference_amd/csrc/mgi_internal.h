@@ -89,8 +89,7 @@ hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan&
 
 // Paged prefill on the matrix cores. `dp` is the padded head dim returned by
 // prefill_head_dim_bucket (0: no MFMA variant); `waves` is 2 or 4; `qpw` is
-// the number of 16-row query blocks per wavefront (2 only with bf16 and
-// waves == 4).
+// the number of 16-row query blocks per wavefront (1).
 int prefill_head_dim_bucket(int dtype_is_bf16, int D);
 hipError_t launch_paged_prefill(const PrefillArgs& a, bool bf16, int dp, int waves, int qpw,
                                 hipStream_t stream);

@@ -8,13 +8,12 @@
 // (minivllm/attention.py:269-299, paged_attention_online) and with the
 // gathered-prefix SDPA of mode sdpa_v2 (minivllm/attention.py:229-267).
 //
-// Work split: one workgroup per (query tile, head); each wavefront owns one
-// or two blocks of 16 query rows. Keys stream through LDS in tiles of 64 (K
+// Work split: one workgroup per (query tile, head); each wavefront owns a
+// block of 16 query rows. Keys stream through LDS in tiles of 64 (K
 // row-major, V transposed, two stages so one barrier per tile suffices).
 // Each wave computes S^T = K Q^T and O^T += V^T P^T with 16x16 MFMA tiles,
 // so a lane's accumulator column is one query row: the online-softmax state
-// (max, sum) is per lane and P needs no transpose. With two query blocks per
-// wave every K and V fragment read from LDS feeds two MFMAs.
+// (max, sum) is per lane and P needs no transpose.
 //
 // Numerics: fp32 accumulation and softmax in the log2 domain; bf16 inputs
 // use v_mfma_f32_16x16x32_bf16 with P rounded to bf16 for the PV product,
@@ -198,18 +197,20 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
       for (int r = 0; r < 4; ++r)
         *reinterpret_cast<uint4*>(&kl[(4 * kq_k + r) * KROW + dc_k * CH]) = kr[j][r];
       if constexpr (kBF16) {
-        // 8 head dims x 4 keys -> eight 4-key runs of V^T rows.
+        // 8 head dims x 4 keys -> eight 4-key runs of V^T rows. Each packed
+        // pair takes the same 16-bit half of one word of two keys' rows
+        // (v_perm_b32 byte select: 0-3 from the second operand, 4-7 from the first).
         const int vc = vt_col_bf16(4 * kq_v);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int w = e >> 1, sh = (e & 1) * 16;
           auto word = [&](const uint4& x) {
-            const uint32_t v = w == 0 ? x.x : w == 1 ? x.y : w == 2 ? x.z : x.w;
-            return (v >> sh) & 0xffffu;
+            const int w = e >> 1;
+            return w == 0 ? x.x : w == 1 ? x.y : w == 2 ? x.z : x.w;
           };
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
           uint2 pk;
-          pk.x = word(vr[j][0]) | (word(vr[j][1]) << 16);
-          pk.y = word(vr[j][2]) | (word(vr[j][3]) << 16);
+          pk.x = __builtin_amdgcn_perm(word(vr[j][1]), word(vr[j][0]), sel);
+          pk.y = __builtin_amdgcn_perm(word(vr[j][3]), word(vr[j][2]), sel);
           *reinterpret_cast<uint2*>(&vl[(8 * dc_v + e) * VROW + vc]) = pk;
         }
       } else {
@@ -348,15 +349,17 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
 
   // ---- pipeline: tile t+1 is in registers while tile t is computed; its
   // block-table slots are in LDS two tiles ahead.
+  // Wave 0 (tid < 64) publishes a tile's K/V row offsets.
+  auto put_slots = [&](int sb, const KeyRows& rows) { slots[sb][tid] = rows; };
   KeyRows slot_next{-1, -1};
   if (tid < kTileKeys) {
-    slots[0][tid] = key_rows(a, tid, kv_end);
+    put_slots(0, key_rows(a, tid, kv_end));
     if (ntiles > 1) slot_next = key_rows(a, kTileKeys + tid, kv_end);
   }
   __syncthreads();
   load_tile(0);
   if (tid < kTileKeys) {
-    slots[1][tid] = slot_next;
+    put_slots(1, slot_next);
     if (ntiles > 2) slot_next = key_rows(a, 2 * kTileKeys + tid, kv_end);
   }
   store_tile(0);
@@ -368,7 +371,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     if (wave_active && kt0 <= wave_last) compute(t & 1, kt0);
     if (t + 1 < ntiles) {
       if (tid < kTileKeys) {
-        slots[t & 1][tid] = slot_next;   // tile t+2
+        put_slots(t & 1, slot_next);   // tile t+2
         if (t + 3 < ntiles) slot_next = key_rows(a, (t + 3) * kTileKeys + tid, kv_end);
       }
       store_tile((t + 1) & 1);
@@ -405,12 +408,7 @@ template <typename T, int DP>
 hipError_t launch_dp(const PrefillArgs& a, int waves, int qpw, hipStream_t stream) {
   const int qb = 16 * waves * qpw;
   const dim3 grid((unsigned)(((int64_t)a.T + qb - 1) / qb * a.H));
-  if constexpr (sizeof(T) == 2) {
-    if (waves == 4 && qpw == 2) {
-      hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 4, 2>), grid, dim3(256), 0, stream, a);
-      return hipGetLastError();
-    }
-  }
+  (void)qpw;  // one 16-row block per wavefront (see launch_paged_prefill)
   if (waves == 4)
     hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 4, 1>), grid, dim3(256), 0, stream, a);
   else
@@ -428,6 +426,11 @@ int prefill_head_dim_bucket(int dtype_is_bf16, int D) {
   return 0;
 }
 
+// Measured on MI355X (bf16, H=16, D=128; chunks of 406-2048 rows after
+// prefixes of 0-2048): four wavefronts of one 16-row block each beat two
+// blocks per wavefront (which holds one wavefront per SIMD, so MFMA and
+// softmax work cannot overlap across wavefronts) and two- or eight-wavefront
+// workgroups, so only QPW == 1 is instantiated.
 hipError_t launch_paged_prefill(const PrefillArgs& a, bool bf16, int dp, int waves, int qpw,
                                 hipStream_t stream) {
   if (bf16) {
