@@ -340,6 +340,35 @@ def cpu_baseline(w):
             "cpu": _cpu_model()}
 
 
+def cpu_prefill_baseline(start: int = 0, T: int = 512, H: int = 16, D: int = 128, S: int = 16):
+    """The prefill oracle (numpy, float32 arithmetic, host BLAS threads) on one
+    chunk of the prefill workload: the CPU restatement of the reference's
+    per-token prefill loop, timed beside the kernel's TFLOP/s."""
+    import numpy as np
+
+    from oracle import paged_decode as ora
+
+    rng = np.random.default_rng(1)
+    nb = -(-(start + T) // S)
+    k = rng.standard_normal((1, nb, S, H, D), dtype=np.float32)
+    v = rng.standard_normal((1, nb, S, H, D), dtype=np.float32)
+    q = rng.standard_normal((T, H, D), dtype=np.float32)
+    table = rng.permutation(nb)
+    times = []
+    for i in range(3):  # 1 warmup + 2 timed
+        t0 = time.perf_counter()
+        ora.paged_prefill(q, k, v, table, start, 0, acc=np.float32)
+        if i:
+            times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    flops = 4 * H * D * (T * start + T * (T + 1) // 2)
+    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or len(os.sched_getaffinity(0))
+    return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "ms": round(sec * 1e3, 2),
+            "cores": threads, "kind": "port",
+            "sample": f"one prefill chunk (start {start}, T {T}, H {H}, D {D}) through "
+                      "oracle.paged_decode.paged_prefill in float32; median of 2 after 1 warmup"}
+
+
 def profiled_traffic(workload: str, split: int):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     counter summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy kernel of
@@ -470,6 +499,7 @@ def main() -> None:
         if not args.no_cpu_baseline:
             log("timing CPU baseline")
             cpu = cpu_baseline(w)
+            cpu["prefill"] = cpu_prefill_baseline()
             log(f"cpu: {cpu}")
 
     workload_tag = f"decode_microbench_{args.dtype}_B{B}_H{H}_D{D}_ctx512-4096"

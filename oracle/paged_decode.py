@@ -261,10 +261,11 @@ def paged_prefill(q, k_pool, v_pool, block_table, start: int, layer: int,
     sc = _scale(D, scale)
     ctx = start + T
     keys, vals = gather_tokens(k_pool, v_pool, np.asarray(block_table)[None, :], ctx, 0, layer, acc)
-    scores = np.einsum("ihd,jhd->hij", q, keys) * sc                      # [H, T, ctx]
+    # Batched over heads: [H, T, D] x [H, D, ctx] -> [H, T, ctx] scores.
+    scores = np.matmul(q.transpose(1, 0, 2), keys.transpose(1, 2, 0)) * sc
     visible = np.arange(ctx)[None, :] <= (start + np.arange(T))[:, None]  # [T, ctx]
     scores = np.where(visible[None], scores, -np.inf)
     scores -= scores.max(axis=-1, keepdims=True)
     w = np.exp(scores)
     w /= w.sum(axis=-1, keepdims=True)
-    return np.einsum("hij,jhd->ihd", w, vals)
+    return np.matmul(w, vals.transpose(1, 0, 2)).transpose(1, 0, 2)       # [T, H, D]
