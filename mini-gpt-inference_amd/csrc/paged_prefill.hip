@@ -117,6 +117,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   __shared__ __align__(16) T k_lds[2][kTileKeys * KROW];
   __shared__ __align__(16) T vt_lds[2][DP * VROW];
   __shared__ KeyRows slots[2][kTileKeys];
+  __shared__ uint64_t slot_valid[2];  // bit k: key k of the tile has K and V rows
 
   // 1-D grid of nq * H workgroups, dispatched round-robin over the XCDs
   // (workgroup id mod 8). With H a multiple of 8, every query tile of head h
@@ -272,38 +273,63 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
       }
     }
 
-    // ---- causal mask (diagonal tiles only), online softmax per query column.
-    // Raw scores s; the log2-domain score is s * scale_log2 (scale > 0, so the
-    // maximum of raw scores gives the maximum of scaled ones).
-    const bool full = kt0 + kTileKeys - 1 <= wave_first;
+    // ---- causal mask (diagonal tiles) and invalid-key mask, online softmax
+    // per query column. Raw scores s; the log2-domain score is s * scale_log2
+    // (scale > 0, so the maximum of raw scores gives the maximum of scaled ones).
+    // The tile's validity mask is wave-uniform: read it into scalar registers
+    // so interior tiles take a branch with no masking work at all.
+    const uint64_t vm_lds = slot_valid[buf];
+    const uint32_t vm_lo = __builtin_amdgcn_readfirstlane((uint32_t)vm_lds);
+    const uint32_t vm_hi = __builtin_amdgcn_readfirstlane((uint32_t)(vm_lds >> 32));
+    const bool full = kt0 + kTileKeys - 1 <= wave_first && (vm_lo & vm_hi) == 0xffffffffu;
     const float c = a.scale_log2;
     float p[QPW][4][4];
+    if (full) {
+#pragma unroll
+      for (int b = 0; b < QPW; ++b)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[b][kb][i] = s[b][kb][i];
+    } else {
+      // This lane's keys are 16*kb + 4*g + i: gather their validity bits once.
+      const uint64_t vm = ((uint64_t)vm_hi << 32) | vm_lo;
+      uint32_t lv = 0;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) lv |= ((uint32_t)(vm >> (16 * kb + 4 * g)) & 0xfu) << (4 * kb);
+#pragma unroll
+      for (int b = 0; b < QPW; ++b)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = kt0 + 16 * kb + 4 * g + i <= qpos[b] && ((lv >> (4 * kb + i)) & 1u);
+            p[b][kb][i] = vis ? s[b][kb][i] : -INFINITY;
+          }
+    }
 #pragma unroll
     for (int b = 0; b < QPW; ++b) {
       float mt = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[b][kb][i] = (full || kt0 + 16 * kb + 4 * g + i <= qpos[b]) ? s[b][kb][i] : -INFINITY;
-          mt = fmaxf(mt, p[b][kb][i]);
-        }
+        for (int i = 0; i < 4; ++i) mt = fmaxf(mt, p[b][kb][i]);
       // The reference maximum (uniform over the four lanes of a column) moves,
       // and the state is rescaled, only when some lane's tile maximum outgrows
-      // it by more than the slack; the first visited tile always sets it (key
-      // 0 is visible to every query, so it is finite). Only then is the
-      // column maximum reduced across lanes.
+      // it by more than the slack; only then is the column maximum reduced
+      // across lanes. A column with nothing visible yet keeps m = -inf and a
+      // zero state.
       mt *= c;
       if (__builtin_amdgcn_ballot_w64(mt > m_run[b] + kRescaleSlack) != 0) {
         mt = cross_group_max(mt);
         const float m_new = fmaxf(m_run[b], mt);
-        const float alpha = fast_exp2(m_run[b] - m_new);
+        const float alpha = m_run[b] == -INFINITY ? 0.f : fast_exp2(m_run[b] - m_new);
         m_run[b] = m_new;
         l_part[b] *= alpha;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) oacc[b][db] *= alpha;
       }
-      const float neg_m = -m_run[b];
+      const float neg_m = m_run[b] == -INFINITY ? 0.f : -m_run[b];
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -356,8 +382,13 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
 
   // ---- pipeline: tile t+1 is in registers while tile t is computed; its
   // block-table slots are in LDS two tiles ahead.
-  // Wave 0 (tid < 64) publishes a tile's K/V row offsets.
-  auto put_slots = [&](int sb, const KeyRows& rows) { slots[sb][tid] = rows; };
+  // Wave 0 (tid < 64, all lanes active) publishes a tile's K/V row offsets
+  // and which of its keys have them.
+  auto put_slots = [&](int sb, const KeyRows& rows) {
+    slots[sb][tid] = rows;
+    const uint64_t vm = __builtin_amdgcn_ballot_w64(rows.k >= 0 && rows.v >= 0);
+    if (tid == 0) slot_valid[sb] = vm;
+  };
   KeyRows slot_next{-1, -1};
   if (tid < kTileKeys) {
     put_slots(0, key_rows(a, tid, kv_end));
@@ -392,7 +423,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   for (int b = 0; b < QPW; ++b) {
     const float l = cross_group_sum(l_part[b]);
     if (qi[b] >= a.T) continue;
-    const float inv = 1.f / l;
+    const float inv = l > 0.f ? 1.f / l : 0.f;  // no visible valid key: zeros
     T* orow = reinterpret_cast<T*>(a.out) + (int64_t)qi[b] * a.o_st + (int64_t)h * a.o_sh;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {

@@ -254,18 +254,28 @@ def paged_prefill(q, k_pool, v_pool, block_table, start: int, layer: int,
     block_table[j // S], offset j % S of `layer`): the result of the
     reference's per-token prefill loop (minivllm/attention.py:269-299), which
     calls paged_attention_online with context_length = start + i + 1. Tokens
-    past start + T - 1 are never read.
+    past start + T - 1 are never read. Tokens whose table entry lies outside
+    [0, N) are masked, and a row left with no visible token is zero.
     """
     q = as_float(q, acc)
     T, H, D = q.shape
+    N, S = k_pool.shape[1], k_pool.shape[2]
     sc = _scale(D, scale)
     ctx = start + T
-    keys, vals = gather_tokens(k_pool, v_pool, np.asarray(block_table)[None, :], ctx, 0, layer, acc)
+    # Token j lives in block table[j // S]; an entry outside [0, N) masks its
+    # tokens (the library's contract; the reference asserts it never happens).
+    pos = np.arange(ctx)
+    blk = np.asarray(block_table, dtype=np.int64)[pos // S]
+    valid = (blk >= 0) & (blk < N)
+    safe = np.where(valid, blk, 0)
+    keys = as_float(k_pool[layer, safe, pos % S], acc)                      # [ctx, H, D]
+    vals = np.where(valid[:, None, None], as_float(v_pool[layer, safe, pos % S], acc), 0.0)
     # Batched over heads: [H, T, D] x [H, D, ctx] -> [H, T, ctx] scores.
     scores = np.matmul(q.transpose(1, 0, 2), keys.transpose(1, 2, 0)) * sc
-    visible = np.arange(ctx)[None, :] <= (start + np.arange(T))[:, None]  # [T, ctx]
+    visible = (pos[None, :] <= (start + np.arange(T))[:, None]) & valid[None, :]  # [T, ctx]
     scores = np.where(visible[None], scores, -np.inf)
-    scores -= scores.max(axis=-1, keepdims=True)
-    w = np.exp(scores)
-    w /= w.sum(axis=-1, keepdims=True)
+    rowmax = scores.max(axis=-1, keepdims=True)
+    w = np.where(visible[None], np.exp(scores - np.where(np.isfinite(rowmax), rowmax, 0.0)), 0.0)
+    den = w.sum(axis=-1, keepdims=True)
+    w = np.divide(w, den, out=np.zeros_like(w), where=den > 0)              # no visible key: zeros
     return np.matmul(w, vals.transpose(1, 0, 2)).transpose(1, 0, 2)       # [T, H, D]

@@ -102,6 +102,23 @@ def test_matches_oracle(start, T, H, D, S, dtype):
     check(out, q, pool, table, start, layer)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_invalid_table_entries_are_masked(dtype):
+    """Entries outside [0, N) mask their block's keys; a row with no visible key is zero."""
+    qkv, pool, table, layer = prefill_case(40, 60, 4, 128, 16, dtype, seed=11)
+    q = qkv.to(DEV)[:, 0]
+    bad = table.clone()
+    bad[1] = -1
+    bad[4] = pool.num_blocks + 7
+    out = run_hip(q, pool, bad, 40, layer)
+    check(out, q, pool, bad, 40, layer)
+    first = table.clone()
+    first[0] = -1
+    out0 = run_hip(q, pool, first, 0, layer)
+    check(out0, q, pool, first, 0, layer)
+    assert torch.count_nonzero(out0[:16]) == 0
+
+
 def test_int32_table_and_contiguous_q_match_int64_and_view():
     qkv, pool, table, layer = prefill_case(37, 50, 4, 128, 16, torch.bfloat16, seed=3)
     q = qkv.to(DEV)[:, 0]

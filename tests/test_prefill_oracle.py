@@ -24,6 +24,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import c_oracle
 from oracle import paged_decode as ora
 
 PIECES = ([5, 7, 19], [1, 1, 9], [16, 1, 15], [8, 8, 8, 8], [3, 5, 4, 16, 11],
@@ -142,3 +143,23 @@ def test_planted_mistakes_are_rejected(bug):
     np.testing.assert_allclose(ora.paged_prefill(q, k, v, table, 28, layer), want, rtol=1e-12)
     bad = _mutant(q, k, v, table, 28, layer, bug)
     assert not np.allclose(np.nan_to_num(bad, nan=1e9), want, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("bad", [[3], [0], [1, 4]], ids=["middle", "first", "two"])
+def test_invalid_table_entries_mask_their_tokens(bad):
+    """Entries outside [0, N) mask their block's tokens; a row that sees none is
+    zero. Pinned by the C decode oracle (an independent restatement that skips
+    such blocks) run once per query row at context start + i + 1."""
+    k, v, table, layer, rng = _case(30, S=4)
+    table = table.copy()
+    for j in bad:
+        table[j] = -1 if j % 2 == 0 else k.shape[1] + 3
+    q = rng.standard_normal((14, 4, 8)).astype(np.float32)
+    got = ora.paged_prefill(q, k, v, table, 16, layer)
+    T = q.shape[0]
+    want = c_oracle.paged_decode(q, k.astype(np.float32), v.astype(np.float32),
+                                 np.repeat(table[None, :], T, axis=0), 16 + np.arange(T) + 1, layer)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    if 0 in bad:
+        start0 = ora.paged_prefill(q, k, v, table, 0, layer)
+        assert np.all(start0[:4] == 0.0)          # rows 0..3 see only the masked block 0
