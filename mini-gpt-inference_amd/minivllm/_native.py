@@ -7,6 +7,7 @@ implementation when the HIP extension is absent.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 
 import torch
@@ -108,10 +109,15 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
-def strides(t: torch.Tensor):
-    """The tensor's element strides as a ctypes int64 array."""
-    st = t.stride()
+@functools.lru_cache(maxsize=1024)
+def _stride_array(st: tuple):
     return (ctypes.c_int64 * len(st))(*st)
+
+
+def strides(t: torch.Tensor):
+    """The tensor's element strides as a ctypes int64 array (cached per stride
+    tuple; the C side only reads it)."""
+    return _stride_array(t.stride())
 
 
 def check(status: int) -> None:
@@ -124,6 +130,12 @@ def check(status: int) -> None:
     raise RuntimeError(f"libminivllm_hip error {status}: {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
     """The HIP stream of torch's current stream on `device`."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
