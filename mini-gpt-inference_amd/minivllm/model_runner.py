@@ -70,7 +70,7 @@ class ModelRunner:
         return logits
 
     def _chunk_index_tensors(self, seq: SequenceState, slots: list[int], context_length: int):
-        """On a GPU pool: the chunk's slots and the sequence's first
+        """With the KV pool on a GPU: the chunk's slots and the sequence's first
         ceil(context_length / S) table entries in one host-to-device copy,
         shared by every layer. On the CPU: (slots, None)."""
         if not self.kv_pool.k.is_cuda:

@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY. This package restates the reference's algorithms
 on the CPU (numpy in paged_decode.py, C in paged_decode_oracle.c) so the HIP
 kernels can be checked against them. Only tests/, __graft_entry__.smoke()
-and bench.py's cpu_baseline leg may import it, and only as the checker or
-the timed CPU baseline -- never as the product path. The minivllm package
+and bench.py's cpu_baseline leg may import it, and only to verify results or
+as the timed CPU baseline -- never as the product path. The minivllm package
 does not import it.
 
 Pinning (see tests/test_oracle_*.py): every function here is checked against

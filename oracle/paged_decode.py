@@ -1,7 +1,7 @@
 """numpy restatement of the paged-KV decode hot path -- TEST INFRASTRUCTURE ONLY.
 
 Imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
-leg, as the checker. Arrays follow the reference layouts:
+leg, to verify results. Arrays follow the reference layouts:
   q            [B, H, D]
   k_pool/v_pool[L, N, S, H, D]
   block_tables [B, M]   (-1 padding in the tail)

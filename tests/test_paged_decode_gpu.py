@@ -1,6 +1,6 @@
 """Parity of the HIP paged decode attention with the CPU oracle (MI355X).
 
-Tolerances (north star): fp32 within 1e-5 (rtol and atol, as the reference
+Tolerances: fp32 within 1e-5 (rtol and atol, as the reference
 tests pair them, tests/test_paged_attention.py:32); bf16 within 2e-2 against
 the oracle evaluated in double on the same bf16 inputs; large logits 5e-4
 (tests/test_triton_paged_decode.py:66-71). Small cases check every element;
