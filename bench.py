@@ -14,8 +14,14 @@ stream the kernels launch on. `cpu_baseline` times the C restatement of the
 reference's online-softmax decode (oracle/paged_decode_oracle.c, fp32
 accumulation) on this host's cores over the same workload.
 
+Extras (skipped with --no-extras) time other decode shapes, the KV append,
+the paged prefill kernel and same-GPU comparisons with the PyTorch backends.
+The end-to-end block (skipped with --no-e2e) runs the full runtime under
+recompute preemption and puts its decode tokens/s in `end_to_end`.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp32]
                        [--split-tokens P] [--no-extras] [--no-cpu-baseline]
+                       [--no-e2e] [--e2e-requests R] [--prefill]
 """
 from __future__ import annotations
 
@@ -46,10 +52,10 @@ def parse_args():
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--no-extras", action="store_true", help="skip the other workload shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--e2e", action="store_true",
-                    help="also run the full runtime under recompute preemption (dim 2048, 12 layers, "
-                         "vocab 32000, bf16, 256 requests, 128 output tokens) with the HIP backend and "
-                         "report decode tokens/s")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the full runtime under recompute preemption (dim 2048, 12 layers, "
+                         "vocab 32000, bf16, 256 requests, 128 output tokens) that reports decode "
+                         "tokens/s")
     ap.add_argument("--e2e-requests", type=int, default=256)
     ap.add_argument("--prefill", action="store_true",
                     help="also time the paged prefill kernel (implied unless --no-extras)")
@@ -126,6 +132,23 @@ def copy_line(mib: int, dev, reps: int = 3):
     return {"mib": mib, "ms": round(ms, 4), "gbps_read_plus_write": round(2 * src.numel() / (ms * 1e-3) / 1e9, 1)}
 
 
+_E2E_MODEL = {}
+
+
+def e2e_model(dev):
+    """The end-to-end model (random init, seed 0, bf16, HIP decode), built once."""
+    import torch
+
+    import _e2e
+
+    if "m" not in _E2E_MODEL:
+        spec = _e2e.RuntimeSpec()
+        model = _e2e.make_model(spec, dev, torch.bfloat16)
+        model.set_decode_attention_backend("hip")
+        _E2E_MODEL["m"] = model
+    return _E2E_MODEL["m"]
+
+
 def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2",
              record_margins: bool = False):
     """The full runtime under recompute preemption with the HIP decode backend
@@ -137,8 +160,8 @@ def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2",
 
     spec = _e2e.RuntimeSpec(n_requests=n_requests, prefill_mode=prefill_mode)
     prompts = _e2e.make_prompts(spec)
-    model = _e2e.make_model(spec, dev, torch.bfloat16)
-    model.set_decode_attention_backend("hip")
+    model = e2e_model(dev)
+    model.set_prefill_fastpath_mode(prefill_mode)
     # warm-up: a few requests through prefill + decode
     warm = _e2e.RuntimeSpec(n_requests=4, output_len=4, seed=99)
     rt, seqs = _e2e.make_runtime(warm, model, _e2e.make_prompts(warm), dev, torch.bfloat16)
@@ -221,8 +244,7 @@ def decode_step_latency(dev, batches=(1, 4, 16, 64, 256), ctx: int = 512, steps:
     from minivllm.kv_block_pool import KVBlockPool
 
     spec = _e2e.RuntimeSpec()
-    model = _e2e.make_model(spec, dev, torch.bfloat16)
-    model.set_decode_attention_backend("hip")
+    model = e2e_model(dev)
     S = spec.block_size
     per_seq = -(-(ctx + 1) // S)
     pool = KVBlockPool(spec.n_layer, max(batches) * per_seq, S, spec.n_head, spec.n_embd // spec.n_head,
@@ -454,14 +476,15 @@ def main() -> None:
             log(f"extra e2e speedup: {extras['e2e_small_model_speedup']}")
             torch.cuda.empty_cache()
 
-        if not args.no_extras or args.e2e or args.prefill:
+        if not args.no_extras or not args.no_e2e or args.prefill:
             for start, T in ((0, 512), (2048, 2048)):
                 key = f"prefill_bf16_start{start}_T{T}_H16_D128"
                 extras[key] = prefill_line(dev, start, T)
                 log(f"extra {key}: {extras[key]}")
             torch.cuda.empty_cache()
 
-        if args.e2e:
+        e2e_summary = None
+        if not args.no_e2e:
             runs = (("e2e_runtime_bf16_preemption", False, "sdpa_v2"),
                     ("e2e_runtime_bf16_preemption_hip_prefill", False, "hip"),
                     ("e2e_runtime_bf16_preemption_hip_prefill_graphs", True, "hip"))
@@ -489,6 +512,12 @@ def main() -> None:
                 extras[key].pop("tokens")
                 log(f"e2e {key}: {extras[key]}")
             extras["decode_step_latency_eager_vs_graph"] = decode_step_latency(dev)
+            hip = extras["e2e_runtime_bf16_preemption_hip_prefill"]
+            e2e_summary = {"decode_tokens_per_s": hip["decode_tok_s_in_decode_phase"],
+                           "output_tokens_per_s": hip["output_tok_s"],
+                           "workload": "full runtime, 256 requests, MiniGPT dim 2048 x 12 layers, bf16, "
+                                       "HIP decode + HIP prefill, recompute preemption"}
+            _E2E_MODEL.clear()
             torch.cuda.empty_cache()
 
         if args.calibrate_copy_mib:
@@ -522,6 +551,7 @@ def main() -> None:
                    "ctx": "U[512,4096]", "sum_ctx": main_line["sum_ctx"], "split_tokens": split},
         "pct_of_peak": main_line["pct_of_peak"],
         "decode_seq_per_s_per_layer": main_line["seq_per_s_per_layer"],
+        "end_to_end": e2e_summary,
         "roofline": {"bound": "hbm", "achieved": main_line["gbps"], "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": round(main_line["gbps"] / PEAK_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
