@@ -236,7 +236,7 @@ def decode_step_latency(dev, batches=(1, 4, 16, 64, 256), ctx: int = 512, steps:
     16 heads, 12 layers, vocab 32000, bf16, HIP decode) at batch B and context
     `ctx`, including metadata packing, the host-to-device copy and the token
     read-back: eager launches against the replay of the step captured for
-    B's bucket (table width fixed at the model's position limit)."""
+    B's bucket at the table width of these contexts."""
     import torch
 
     import _e2e
@@ -269,7 +269,7 @@ def decode_step_latency(dev, batches=(1, 4, 16, 64, 256), ctx: int = 512, steps:
         def replay():
             return graphs.run(tokens, positions, slots, tables)[1]
 
-        graphs.capture(B)
+        graphs.capture(B, graphs.width(per_seq))
         res = {}
         for name, fn in (("eager", eager), ("graph", replay)):
             for _ in range(3):

@@ -4,12 +4,15 @@ LM head and the greedy argmax) recorded once per batch-size bucket as a HIP
 graph and replayed each step.
 
 A step's metadata (input ids, positions, context lengths, slot mapping and
-block tables) lives in one static int64 device buffer per bucket; a step
-fills it with a single host-to-device copy and replays. The block-table
-width is fixed at the most blocks one sequence can hold, so one graph per
-batch bucket serves every context length. Rows past the real batch are
-padding: slot -1 (the KV append skips them), context length 0 (attention
-writes zeros), token and position 0; their logits are discarded.
+block tables) lives in one static int64 device buffer per graph; a step
+fills it with a single host-to-device copy and replays. Graphs are keyed by
+(batch bucket, table-width bucket): the width is the smallest power of two
+(at least 16) or the position limit in blocks that holds the batch's
+longest table, so the attention grid is sized for the contexts actually
+present. Rows past the real batch are padding: slot -1 (the KV append skips
+them), context length 0 (attention writes zeros), token and position 0; their
+logits are discarded. All graphs of one DecodeGraphs share one memory pool
+(they never run concurrently).
 
 Capture needs the HIP decode backend: the PyTorch reference backend reads
 device data on the host while filtering padding slots, which a graph cannot
@@ -24,10 +27,11 @@ from .decode_batch_metadata import DecodeBatchMetadata
 from .kv_block_pool import KVBlockPool
 
 # Batch buckets captured by default. On MI355X a replayed step of the
-# dim-2048, 12-layer model (context 512) takes 1.35 ms against 2.3 ms of eager
-# launches up to 16 rows and 2.05 against 2.33 ms at 64 rows; at 256 rows the
-# step is bound by the GPU and the padded replay is slightly slower (4.44 vs
-# 4.24 ms), so larger batches run eagerly.
+# dim-2048, 12-layer model at context 512 takes 1.3 ms against 2.1-2.2 ms of
+# eager launches up to 16 rows and 1.86 against 2.16 ms at 64 rows. At 256
+# rows the step is bound by the GPU (4.27 vs 4.24 ms), and in the full
+# preemption runtime padding 129-256-row batches to 256 made the decode phase
+# 25% slower than eager, so larger batches run eagerly.
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64)
 
 
@@ -62,8 +66,18 @@ def metadata_views(buf: torch.Tensor, B_pad: int, M: int):
     return buf[0:B_pad].view(B_pad, 1), meta
 
 
+def width_buckets(max_blocks: int) -> tuple[int, ...]:
+    """Table widths graphs are captured for: powers of two from 16 below
+    max_blocks, then max_blocks."""
+    out, w = [], 16
+    while w < max_blocks:
+        out.append(w)
+        w *= 2
+    return tuple(out) + (max_blocks,)
+
+
 class _Captured:
-    def __init__(self, model, pool: KVBlockPool, B_pad: int, M: int):
+    def __init__(self, model, pool: KVBlockPool, B_pad: int, M: int, mempool):
         dev = pool.k.device
         self.B_pad, self.M = B_pad, M
         self.buf = pack_decode_metadata([], [], [], [], B_pad, M).to(dev)
@@ -76,7 +90,7 @@ class _Captured:
                     model.decode_batch(input_ids=ids, metadata=meta, kv_pool=pool)
             torch.cuda.current_stream(dev).wait_stream(side)
             self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
+            with torch.cuda.graph(self.graph, pool=mempool):
                 logits = model.decode_batch(input_ids=ids, metadata=meta, kv_pool=pool)
                 self.logits = logits[:, -1, :]
                 self.tokens = torch.argmax(self.logits, dim=-1)
@@ -103,21 +117,30 @@ class DecodeGraphs:
             raise ValueError("max_blocks_per_seq must be positive")
         self.model, self.pool, self.M = model, pool, int(max_blocks_per_seq)
         self.buckets = tuple(sorted(buckets))
-        self._graphs: dict[int, _Captured] = {}
+        self.widths = width_buckets(self.M)
+        self._graphs: dict[tuple[int, int], _Captured] = {}
+        self._mempool = torch.cuda.graph_pool_handle()
 
     def bucket(self, B: int) -> int | None:
         return next((b for b in self.buckets if b >= B), None)
 
-    def capture(self, B_pad: int) -> None:
-        if B_pad not in self._graphs:
-            self._graphs[B_pad] = _Captured(self.model, self.pool, B_pad, self.M)
+    def width(self, max_len: int) -> int | None:
+        return next((w for w in self.widths if w >= max_len), None)
+
+    def capture(self, B_pad: int, width: int | None = None) -> None:
+        """Captures the graph of batch bucket B_pad at one table width (default:
+        every width bucket)."""
+        for w in (self.widths if width is None else (width,)):
+            if (B_pad, w) not in self._graphs:
+                self._graphs[(B_pad, w)] = _Captured(self.model, self.pool, B_pad, w, self._mempool)
 
     def run(self, tokens, positions, slots, tables):
         """One decode step for len(tokens) rows; None if no bucket fits."""
         B = len(tokens)
         B_pad = self.bucket(B)
-        if B_pad is None or max(len(t) for t in tables) > self.M:
+        W = self.width(max(len(t) for t in tables))
+        if B_pad is None or W is None:
             return None
-        self.capture(B_pad)
-        host = pack_decode_metadata(tokens, positions, slots, tables, B_pad, self.M)
-        return self._graphs[B_pad].replay(host, B)
+        self.capture(B_pad, W)
+        host = pack_decode_metadata(tokens, positions, slots, tables, B_pad, W)
+        return self._graphs[(B_pad, W)].replay(host, B)

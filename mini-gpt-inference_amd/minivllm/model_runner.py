@@ -98,18 +98,20 @@ class ModelRunner:
 
     def enable_decode_graphs(self, max_blocks_per_seq: int | None = None,
                              buckets: tuple[int, ...] | None = None) -> None:
-        """Replays decode steps from HIP graphs captured per batch-size bucket.
+        """Replays decode steps from HIP graphs captured per (batch-size bucket,
+        block-table width bucket), capturing each on first use.
 
-        Needs the model on a GPU with the hip decode backend. The block-table
-        width is fixed at ``max_blocks_per_seq`` (default: the model's
-        position limit in blocks); steps that do not fit a bucket run eagerly.
+        Needs the model on a GPU with the hip decode backend. Widths go up to
+        ``max_blocks_per_seq`` (default: the model's position limit in
+        blocks); steps that fit no bucket run eagerly.
         """
         M = max_blocks_per_seq or -(-self.model.block_size // self.kv_pool.block_size)
         self._decode_graphs = DecodeGraphs(self.model, self.kv_pool, M,
                                            buckets if buckets is not None else DEFAULT_BUCKETS)
 
     def capture_decode_graphs(self, batch_sizes) -> None:
-        """Captures the buckets for these batch sizes now (e.g. before timing)."""
+        """Captures the buckets for these batch sizes at every table width now
+        (e.g. before timing)."""
         for B in batch_sizes:
             b = self._decode_graphs.bucket(B)
             if b is not None:
