@@ -145,3 +145,11 @@ def test_status_mapping_to_python_exceptions():
 def test_dtype_codes_cover_supported_types():
     assert set(_native.DTYPE_CODES) == {torch.float32, torch.bfloat16, torch.float16}
     assert set(_native.ITYPE_CODES) == {torch.int32, torch.int64}
+
+
+def test_missing_library_raises_runtime_error(monkeypatch, tmp_path):
+    """No silent fallback: without the built library every entry point raises."""
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "library_path", lambda: tmp_path / "libminivllm_hip.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.lib()
