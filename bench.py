@@ -464,6 +464,11 @@ def main() -> None:
             extras["longctx_bf16_B8_ctx32k-128k"] = decode_line(w4, max(5, args.steps // 5), 2, 0)
             del w4
             log(f"extra longctx: {extras['longctx_bf16_B8_ctx32k-128k']}")
+            w5 = fx.make_decode_workload(256, H, D, S, 32768, 128, 2048, torch.bfloat16, dev, seed=0,
+                                         poison=False)
+            extras["decode_bf16_B256_ctx128-2048"] = decode_line(w5, max(5, args.steps // 2), 3, 0)
+            del w5
+            log(f"extra B256: {extras['decode_bf16_B256_ctx128-2048']}")
             extras["kv_append_bf16_B256"] = append_line(max(20, args.steps), 5, dev)
             log(f"extra append: {extras['kv_append_bf16_B256']}")
             extras["d2d_copy_4GiB"] = copy_line(4096, dev, reps=5)
