@@ -234,13 +234,15 @@ def prefill_line(dev, start: int, T: int, H: int = 16, D: int = 128, steps: int 
 def decode_step_latency(dev, batches=(1, 4, 16, 64, 256), ctx: int = 512, steps: int = 20):
     """Wall time of one greedy decode step of the end-to-end model (dim 2048,
     16 heads, 12 layers, vocab 32000, bf16, HIP decode) at batch B and context
-    `ctx`, including metadata packing, the host-to-device copy and the token
-    read-back: eager launches against the replay of the step captured for
-    B's bucket at the table width of these contexts."""
+    `ctx`, through the runtime's own step preparation (staging against the
+    device-resident block tables, one host-to-device copy) and including the
+    token read-back: eager launches against the replay of the step captured
+    for B's bucket at the table width of these contexts."""
     import torch
 
     import _e2e
-    from minivllm.decode_graphs import DecodeGraphs, metadata_views, pack_decode_metadata
+    from minivllm.decode_graphs import DecodeGraphs, pack_decode_step, step_metadata
+    from minivllm.device_block_tables import DeviceBlockTables
     from minivllm.kv_block_pool import KVBlockPool
 
     spec = _e2e.RuntimeSpec()
@@ -256,20 +258,29 @@ def decode_step_latency(dev, batches=(1, 4, 16, 64, 256), ctx: int = 512, steps:
     out = {}
     for B in batches:
         tables = [list(range(b * per_seq, (b + 1) * per_seq)) for b in range(B)]
+        seq_ids = [f"s{b}" for b in range(B)]
         tokens = [(7 * b + 3) % spec.vocab for b in range(B)]
         positions = [ctx] * B
         slots = [t[ctx // S] * S + ctx % S for t in tables]
+        dtab = DeviceBlockTables(dev, cols=M_graph)
+
+        def stage(B_pad):
+            rows, upd = dtab.stage(seq_ids, tables)
+            step = pack_decode_step(tokens, positions, slots, rows, upd, B_pad).to(dev)
+            dtab.apply(step[5 * B_pad:])
+            return step
 
         def eager():
-            buf = pack_decode_metadata(tokens, positions, slots, tables, B, per_seq).to(dev)
-            ids, meta = metadata_views(buf, B, per_seq)
+            ids, meta = step_metadata(stage(B), B, dtab, per_seq)
             logits = model.decode_batch(ids, meta, pool)[:, -1, :]
             return torch.argmax(logits, dim=-1).tolist()
 
-        def replay():
-            return graphs.run(tokens, positions, slots, tables)[1]
+        key = graphs.target(B, per_seq)
 
-        graphs.capture(B, graphs.width(per_seq))
+        def replay():
+            return graphs.replay_staged(key, stage(key[0]), B, dtab)[1]
+
+        graphs.capture(*key)
         res = {}
         for name, fn in (("eager", eager), ("graph", replay)):
             for _ in range(3):
@@ -283,6 +294,56 @@ def decode_step_latency(dev, batches=(1, 4, 16, 64, 256), ctx: int = 512, steps:
                         "speedup": round(res["eager"] / res["graph"], 2)}
         log(f"decode step latency B={B} ctx={ctx}: {out[f'B{B}']}")
     return {"ctx": ctx, "by_batch": out}
+
+
+def metadata_prep_line(dev, steps: int = 50):
+    """Host-to-device preparation of one decode step's metadata, synchronised:
+    every -1 padded table built on the host and copied in the step's one copy
+    (pack_decode_metadata) against device-resident tables that receive only
+    changed entries (DeviceBlockTables). A sixteenth of the rows gains a block
+    every step, as in steady decoding with block size 16."""
+    import torch
+
+    from minivllm.decode_graphs import metadata_views, pack_decode_metadata, pack_decode_step, step_metadata
+    from minivllm.device_block_tables import DeviceBlockTables
+
+    out = {}
+    for B, ctx in ((64, 512), (256, 512), (256, 2048)):
+        nb = ctx // 16 + 1
+        g = torch.Generator().manual_seed(B + ctx)
+        perm = torch.randperm(B * (nb + steps), generator=g).tolist()
+        tables = [perm[b * nb:(b + 1) * nb] for b in range(B)]
+        spare = iter(perm[B * nb:])
+        seq_ids = [f"s{b}" for b in range(B)]
+        tokens, positions, slots = list(range(B)), [ctx] * B, [t[-1] * 16 for t in tables]
+        dtab = DeviceBlockTables(dev, cols=2 * nb)
+
+        def host_built():
+            M = max(len(t) for t in tables)
+            return metadata_views(pack_decode_metadata(tokens, positions, slots, tables, B, M).to(dev), B, M)
+
+        def device_resident():
+            rows, upd = dtab.stage(seq_ids, tables)
+            step = pack_decode_step(tokens, positions, slots, rows, upd, B).to(dev)
+            dtab.apply(step[5 * B:])
+            return step_metadata(step, B, dtab, max(len(t) for t in tables))
+
+        res = {}
+        for name, fn in (("host_built_ms", host_built), ("device_resident_ms", device_resident)):
+            fn()  # the first device-resident step uploads every table
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(steps):
+                for t in tables[(i % 16) * B // 16:(i % 16 + 1) * B // 16]:
+                    t.append(next(spare))
+                meta = fn()[1]
+                torch.cuda.synchronize()
+            res[name] = round((time.perf_counter() - t0) / steps * 1e3, 3)
+            M = max(len(t) for t in tables)
+            assert meta.block_tables.tolist() == [t + [-1] * (M - len(t)) for t in tables]
+        out[f"B{B}_ctx{ctx}"] = res
+        log(f"metadata prep B={B} ctx={ctx}: {res}")
+    return out
 
 
 def attention_speedup_grid(dev):
@@ -517,6 +578,7 @@ def main() -> None:
                 extras[key].pop("tokens")
                 log(f"e2e {key}: {extras[key]}")
             extras["decode_step_latency_eager_vs_graph"] = decode_step_latency(dev)
+            extras["decode_metadata_prep"] = metadata_prep_line(dev)
             hip = extras["e2e_runtime_bf16_preemption_hip_prefill"]
             e2e_summary = {"decode_tokens_per_s": hip["decode_tok_s_in_decode_phase"],
                            "output_tokens_per_s": hip["output_tok_s"],

@@ -4,8 +4,10 @@ LM head and the greedy argmax) recorded once per batch-size bucket as a HIP
 graph and replayed each step.
 
 A step's metadata (input ids, positions, context lengths, slot mapping and
-block tables) lives in one static int64 device buffer per graph; a step
-fills it with a single host-to-device copy and replays. Graphs are keyed by
+block tables) lives in one static int64 device buffer per graph. The runtime
+fills it from one host-to-device copy of the step's scalars and table
+updates (``pack_decode_step``), gathering the tables from the device-resident
+``DeviceBlockTables``; ``run`` fills it from a host-built buffer instead. Graphs are keyed by
 (batch bucket, table-width bucket): the width is the smallest power of two
 (at least 16) or the position limit in blocks that holds the batch's
 longest table, so the attention grid is sized for the contexts actually
@@ -66,6 +68,39 @@ def metadata_views(buf: torch.Tensor, B_pad: int, M: int):
     return buf[0:B_pad].view(B_pad, 1), meta
 
 
+def pack_decode_step(tokens, positions, slots, rows, updates, B_pad: int) -> torch.Tensor:
+    """Host int64 buffer [ids | positions | context_lengths | slots | table rows |
+    table updates] of one decode step for B_pad rows. ``rows`` and ``updates``
+    come from DeviceBlockTables.stage; padding rows get token and position 0,
+    context 0, slot -1 and table row 0 (all -1)."""
+    B = len(tokens)
+    host = np.empty(5 * B_pad + len(updates), dtype=np.int64)
+    host[:3 * B_pad] = 0
+    host[3 * B_pad:4 * B_pad] = -1
+    host[4 * B_pad:5 * B_pad] = 0
+    if B:
+        host[:B] = tokens
+        host[B_pad:B_pad + B] = positions
+        host[2 * B_pad:2 * B_pad + B] = host[B_pad:B_pad + B] + 1
+        host[3 * B_pad:3 * B_pad + B] = slots
+        host[4 * B_pad:4 * B_pad + B] = rows
+    host[5 * B_pad:] = updates
+    return torch.from_numpy(host)
+
+
+def step_metadata(buf: torch.Tensor, B: int, tables, M: int):
+    """(input_ids [B,1], DecodeBatchMetadata) of a device copy of
+    pack_decode_step(..., B_pad=B) after tables.apply(buf[5B:]); the block
+    tables are a fresh [B, M] gather of the device-resident rows."""
+    meta = DecodeBatchMetadata(
+        positions=buf[B:2 * B],
+        context_lengths=buf[2 * B:3 * B],
+        block_tables=tables.gather(buf[4 * B:5 * B], M),
+        slot_mapping=buf[3 * B:4 * B],
+    )
+    return buf[0:B].view(B, 1), meta
+
+
 def width_buckets(max_blocks: int) -> tuple[int, ...]:
     """Table widths graphs are captured for: powers of two from 16 below
     max_blocks, then max_blocks."""
@@ -97,6 +132,15 @@ class _Captured:
 
     def replay(self, host: torch.Tensor, B: int):
         self.buf.copy_(host)
+        self.graph.replay()
+        return self.logits[:B].clone(), self.tokens[:B].tolist()
+
+    def replay_staged(self, step: torch.Tensor, B: int, tables):
+        """Replays from a device copy of pack_decode_step(..., B_pad) whose
+        table updates are applied."""
+        n = 4 * self.B_pad
+        self.buf[:n].copy_(step[:n])
+        tables.gather_into(step[n:n + self.B_pad], self.buf[n:].view(self.B_pad, self.M))
         self.graph.replay()
         return self.logits[:B].clone(), self.tokens[:B].tolist()
 
@@ -133,6 +177,17 @@ class DecodeGraphs:
         for w in (self.widths if width is None else (width,)):
             if (B_pad, w) not in self._graphs:
                 self._graphs[(B_pad, w)] = _Captured(self.model, self.pool, B_pad, w, self._mempool)
+
+    def target(self, B: int, max_len: int) -> tuple[int, int] | None:
+        """(batch bucket, width bucket) of a step, or None if none fits."""
+        B_pad, W = self.bucket(B), self.width(max_len)
+        return None if B_pad is None or W is None else (B_pad, W)
+
+    def replay_staged(self, key: tuple[int, int], step: torch.Tensor, B: int, tables):
+        """One decode step of B rows from a device copy of pack_decode_step
+        (padded to key[0] rows, table updates applied)."""
+        self.capture(*key)
+        return self._graphs[key].replay_staged(step, B, tables)
 
     def run(self, tokens, positions, slots, tables):
         """One decode step for len(tokens) rows; None if no bucket fits."""

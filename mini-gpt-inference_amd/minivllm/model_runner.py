@@ -4,12 +4,15 @@
 block), builds DecodeBatchMetadata, runs one batched decode step, commits
 ``length += 1`` and returns ``(logits[:, -1, :], greedy next tokens)``.
 
-The metadata of a step (input ids, positions, context lengths, slot
-mapping and the -1 padded block tables) is packed into one int64 host
-buffer and moved with a single host-to-device copy; every field is a
-contiguous view of that device buffer. The reference issues about B + 5
-separate copies (one per block-table row, minivllm/model_runner.py:191-201).
-With ``enable_decode_graphs`` the step replays a captured HIP graph instead
+The metadata of a step (input ids, positions, context lengths and slot
+mapping) is packed into one int64 host buffer together with the block-table
+entries that changed since the last step, and moved with a single
+host-to-device copy. Block tables stay resident on the device, one row per
+sequence (minivllm.device_block_tables): the copy applies the changed entries
+and one gather builds the batch's -1 padded [B, M] table. The reference
+rebuilds every table on the host and issues about B + 5 separate copies (one
+per block-table row, minivllm/model_runner.py:176-214). With
+``enable_decode_graphs`` the step replays a captured HIP graph instead
 (minivllm.decode_graphs).
 """
 from __future__ import annotations
@@ -17,7 +20,8 @@ from __future__ import annotations
 import torch
 
 from .block_manager import BlockManager
-from .decode_graphs import DEFAULT_BUCKETS, DecodeGraphs, metadata_views, pack_decode_metadata
+from .decode_graphs import DEFAULT_BUCKETS, DecodeGraphs, pack_decode_step, step_metadata
+from .device_block_tables import DeviceBlockTables
 from .kv_block_pool import KVBlockPool
 from .kv_runtime import KVRuntimeContext, PrefillChunkContext, PrefillRuntimeContext
 from .model import MiniGPT
@@ -88,13 +92,30 @@ class ModelRunner:
         return ([seq.last_token for seq in sequences], [seq.length for seq in sequences], slots,
                 [seq.block_table for seq in sequences])
 
+    def _device_tables(self) -> DeviceBlockTables:
+        tables = getattr(self, "_block_tables", None)
+        if tables is None:
+            cols = -(-self.model.block_size // self.kv_pool.block_size)
+            tables = self._block_tables = DeviceBlockTables(self.device, cols=cols)
+        return tables
+
+    def _stage_decode_step(self, sequences, rows, B_pad: int) -> torch.Tensor:
+        """Device copy of this step's packed metadata for B_pad rows, with the
+        block-table updates applied to the device-resident tables."""
+        tokens, positions, slots, tables = rows
+        dt = self._device_tables()
+        table_rows, updates = dt.stage([seq.seq_id for seq in sequences], tables)
+        step = pack_decode_step(tokens, positions, slots, table_rows, updates, B_pad).to(self.device)
+        dt.apply(step[5 * B_pad:])
+        return step
+
     def _prepare_decode_batch(self, sequences: list[SequenceState]):
         B = len(sequences)
         assert B > 0
-        tokens, positions, slots, tables = self._reserve_decode_rows(sequences)
-        M = max(len(t) for t in tables)
-        dev = pack_decode_metadata(tokens, positions, slots, tables, B, M).to(self.device)
-        return metadata_views(dev, B, M)
+        rows = self._reserve_decode_rows(sequences)
+        M = max(len(t) for t in rows[3])
+        step = self._stage_decode_step(sequences, rows, B)
+        return step_metadata(step, B, self._device_tables(), M)
 
     def enable_decode_graphs(self, max_blocks_per_seq: int | None = None,
                              buckets: tuple[int, ...] | None = None) -> None:
@@ -132,23 +153,19 @@ class ModelRunner:
     def decode_batch(self, sequences: list[SequenceState]):
         if not sequences:
             return []
+        B = len(sequences)
+        rows = self._reserve_decode_rows(sequences)
+        M = max(len(t) for t in rows[3])
         graphs = getattr(self, "_decode_graphs", None)
-        if graphs is not None:
-            rows = self._reserve_decode_rows(sequences)
-            out = graphs.run(*rows)
-            if out is None:  # no bucket fits: run this step eagerly with the same slots
-                B, M = len(sequences), max(len(t) for t in rows[3])
-                dev = pack_decode_metadata(*rows, B, M).to(self.device)
-                input_ids, metadata = metadata_views(dev, B, M)
-                logits = self.model.decode_batch(input_ids=input_ids, metadata=metadata, kv_pool=self.kv_pool)
-                last = logits[:, -1, :]
-                out = (last, torch.argmax(last, dim=-1).tolist())
-            for seq in sequences:
-                seq.length += 1
-            return out
-        input_ids, metadata = self._prepare_decode_batch(sequences=sequences)
-        logits = self.model.decode_batch(input_ids=input_ids, metadata=metadata, kv_pool=self.kv_pool)
+        key = graphs.target(B, M) if graphs is not None else None
+        step = self._stage_decode_step(sequences, rows, key[0] if key else B)
+        if key is not None:
+            out = graphs.replay_staged(key, step, B, self._device_tables())
+        else:  # eager (also when no graph bucket fits)
+            input_ids, metadata = step_metadata(step, B, self._device_tables(), M)
+            logits = self.model.decode_batch(input_ids=input_ids, metadata=metadata, kv_pool=self.kv_pool)
+            last = logits[:, -1, :]
+            out = (last, torch.argmax(last, dim=-1).tolist())
         for seq in sequences:
             seq.length += 1
-        last = logits[:, -1, :]
-        return last, torch.argmax(last, dim=-1).tolist()
+        return out
