@@ -176,7 +176,7 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   DecodePlan plan{};
   plan.path = DecodePath::kGeneric;
   const int64_t row_span = ((H - 1) * std::max(k_pool_strides[3], v_pool_strides[3]) + D) * eb;
-  if ((dtype == MGI_BF16 || dtype == MGI_F32) && D % 8 == 0 && D <= 256 &&
+  if (D % 8 == 0 && D <= 256 &&
       k_pool_strides[4] == 1 && v_pool_strides[4] == 1 && aligned16(kbase) &&
       aligned16(vbase) && mult16(k_pool_strides[1], eb) && mult16(k_pool_strides[2], eb) &&
       mult16(k_pool_strides[3], eb) && mult16(v_pool_strides[1], eb) &&
@@ -185,9 +185,11 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
       std::max(k_pool_strides[2], v_pool_strides[2]) * eb * S < (int64_t(1) << 31)) {
     int tok = 0;
     const int want = tokens_per_step_override();
-    const int def = dtype == MGI_BF16 ? 16 : 8;
+    const bool two_byte = dtype != MGI_F32;
+    const int def = two_byte ? 16 : 8;
     for (int t : {want, def, 8, 4}) {
-      if (t > 0 && (t == 4 || t == 8 || (t == 16 && dtype == MGI_BF16)) && S % t == 0) {
+      if (t > 0 && ((two_byte && (t == 8 || t == 16)) || (!two_byte && (t == 4 || t == 8))) &&
+          S % t == 0) {
         tok = t;
         break;
       }
@@ -358,10 +360,9 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
   const int64_t eb = dtype_bytes(dtype);
   const char* kbase = static_cast<const char*>(k_pool) + layer_idx * k_pool_strides[0] * eb;
   const char* vbase = static_cast<const char*>(v_pool) + layer_idx * v_pool_strides[0] * eb;
-  const bool bf16 = dtype == MGI_BF16;
-  const int dp = (dtype == MGI_BF16 || dtype == MGI_F32) ? prefill_head_dim_bucket(bf16, (int)D) : 0;
+  const int dp = prefill_head_dim_bucket(dtype != MGI_F32, (int)D);
 
-  // Matrix-core path: bf16 or f32, head dim a multiple of one 16-byte chunk
+  // Matrix-core path: head dim a multiple of one 16-byte chunk
   // within the padded bucket, unit head-dim strides, 16-byte aligned rows.
   const bool mfma = dp != 0 && D % (16 / eb) == 0 && q_strides[2] == 1 && out_strides[2] == 1 &&
                     k_pool_strides[4] == 1 && v_pool_strides[4] == 1 && aligned16(q) &&
@@ -404,7 +405,7 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
     // Four wavefronts of 16 query rows share each staged K/V tile; chunks of
     // at most 32 rows use two.
     const int waves = T <= 32 ? 2 : 4;
-    e = launch_paged_prefill(a, bf16, dp, waves, 1, st);
+    e = launch_paged_prefill(a, dtype, dp, waves, 1, st);
   } else {
     // Any other shape: the chunk as T single-query rows of the generic decode
     // kernel, sharing one table row, with context lengths start_pos + t + 1.

@@ -90,8 +90,8 @@ hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan&
 // Paged prefill on the matrix cores. `dp` is the padded head dim returned by
 // prefill_head_dim_bucket (0: no MFMA variant); `waves` is 2 or 4; `qpw` is
 // the number of 16-row query blocks per wavefront (1).
-int prefill_head_dim_bucket(int dtype_is_bf16, int D);
-hipError_t launch_paged_prefill(const PrefillArgs& a, bool bf16, int dp, int waves, int qpw,
+int prefill_head_dim_bucket(int two_byte, int D);
+hipError_t launch_paged_prefill(const PrefillArgs& a, int dtype, int dp, int waves, int qpw,
                                 hipStream_t stream);
 
 // KV append launchers. `vector_path` copies 16-byte chunks (same dtype,

@@ -22,8 +22,9 @@
 // partials that paged_decode_merge combines:
 //   M = max_p m_p,  L = sum_p l_p 2^(m_p - M),  O = sum_p O_p 2^(m_p - M) / L.
 //
-// Generic path (paged_decode_generic): any strides, head_dim up to 512, any
-// block size, f32/bf16/f16; one wavefront per (b, h), one token at a time.
+// The fast path covers bf16, f16 (the same lane layout, v_dot2_f32_f16) and
+// f32. Generic path (paged_decode_generic): any strides, head_dim up to 512,
+// any block size, f32/bf16/f16; one wavefront per (b, h), one token at a time.
 #include "mgi_common.h"
 #include "mgi_internal.h"
 #include "minivllm_hip.h"
@@ -41,6 +42,7 @@ template <> struct Layout<bf16_t> {
   __device__ static int load_off(int sub, int /*D*/, int /*j*/) { return 8 * sub; }
   __device__ static int elem(int sub, int /*D*/, int i) { return 8 * sub + i; }
 };
+template <> struct Layout<f16_t> : Layout<bf16_t> {};
 template <> struct Layout<float> {
   static constexpr int kLoads = 2;
   __device__ static int load_off(int sub, int D, int j) { return j * (D >> 1) + 4 * sub; }
@@ -48,6 +50,7 @@ template <> struct Layout<float> {
 };
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // Element i (0..7) of a lane's raw fragment as f32.
 template <typename T>
@@ -58,39 +61,53 @@ __device__ __forceinline__ float frag_elem<bf16_t>(const uint4 (&r)[1], int i) {
   return (i & 1) ? bf16_hi(w) : bf16_lo(w);
 }
 template <>
+__device__ __forceinline__ float frag_elem<f16_t>(const uint4 (&r)[1], int i) {
+  const uint32_t w = (i >> 1) == 0 ? r[0].x : (i >> 1) == 1 ? r[0].y : (i >> 1) == 2 ? r[0].z : r[0].w;
+  return f16_to_f32((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+template <>
 __device__ __forceinline__ float frag_elem<float>(const uint4 (&r)[2], int i) {
   const uint4& x = r[i >> 2];
   const uint32_t w = (i & 3) == 0 ? x.x : (i & 3) == 1 ? x.y : (i & 3) == 2 ? x.z : x.w;
   return __uint_as_float(w);
 }
 
-// Query fragment: packed bf16 pairs (exact) for bf16, f32 values for f32.
+// Query fragment: packed 16-bit pairs (exact) for bf16 and f16, f32 values
+// for f32. The 2-byte types dot with v_dot2_f32_bf16 / v_dot2_f32_f16 (f32
+// accumulate; the products of two 16-bit values are exact in f32).
 template <typename T> struct QFrag;
-template <> struct QFrag<bf16_t> {
+template <typename T>
+struct QFrag16 {
   uint32_t w[4];
+  __device__ static __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (sizeof(T) == 2 && __is_same(T, bf16_t))
+      return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                             __builtin_bit_cast(bf16x2, b), c, false);
+    else
+      return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                    false);
+  }
   __device__ __forceinline__ float dot(const uint4 (&k)[1]) const {
     float d = 0.f;
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[0]),
-                                        __builtin_bit_cast(bf16x2, k[0].x), d, false);
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[1]),
-                                        __builtin_bit_cast(bf16x2, k[0].y), d, false);
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[2]),
-                                        __builtin_bit_cast(bf16x2, k[0].z), d, false);
-    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[3]),
-                                        __builtin_bit_cast(bf16x2, k[0].w), d, false);
+    d = dot2(w[0], k[0].x, d);
+    d = dot2(w[1], k[0].y, d);
+    d = dot2(w[2], k[0].z, d);
+    d = dot2(w[3], k[0].w, d);
     return d;
   }
-  __device__ __forceinline__ void load(const bf16_t* row, int64_t sd, int sub, int D) {
+  __device__ __forceinline__ void load(const T* row, int64_t sd, int sub, int D) {
     const uint16_t* p = reinterpret_cast<const uint16_t*>(row);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = p[(int64_t)Layout<bf16_t>::elem(sub, D, 2 * j) * sd];
-      const uint32_t hi = p[(int64_t)Layout<bf16_t>::elem(sub, D, 2 * j + 1) * sd];
+      const uint32_t lo = p[(int64_t)Layout<T>::elem(sub, D, 2 * j) * sd];
+      const uint32_t hi = p[(int64_t)Layout<T>::elem(sub, D, 2 * j + 1) * sd];
       w[j] = lo | (hi << 16);
     }
   }
   __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = 0u; }
 };
+template <> struct QFrag<bf16_t> : QFrag16<bf16_t> {};
+template <> struct QFrag<f16_t> : QFrag16<f16_t> {};
 template <> struct QFrag<float> {
   float f[8];
   __device__ __forceinline__ float dot(const uint4 (&k)[2]) const {
@@ -486,6 +503,7 @@ hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan&
   if (plan.path == DecodePath::kFast) {
     if (dtype == MGI_BF16) return launch_fast<bf16_t>(a, plan, stream);
     if (dtype == MGI_F32) return launch_fast<float>(a, plan, stream);
+    if (dtype == MGI_F16) return launch_fast<f16_t>(a, plan, stream);
     return hipErrorInvalidValue;
   }
   if (dtype == MGI_BF16) return launch_generic<bf16_t>(a, stream);

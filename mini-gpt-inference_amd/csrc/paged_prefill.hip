@@ -15,16 +15,17 @@
 // so a lane's accumulator column is one query row: the online-softmax state
 // (max, sum) is per lane and P needs no transpose.
 //
-// Numerics: fp32 accumulation and softmax in the log2 domain; bf16 inputs
-// use v_mfma_f32_16x16x32_bf16 with P rounded to bf16 for the PV product,
-// fp32 inputs use v_mfma_f32_16x16x4_f32 (full fp32 products).
+// Numerics: fp32 accumulation and softmax in the log2 domain; bf16 and f16
+// inputs use v_mfma_f32_16x16x32_bf16 / _f16 with P rounded to the input
+// type for the PV product, fp32 inputs use v_mfma_f32_16x16x4_f32 (full fp32
+// products).
 #include "mgi_common.h"
 #include "mgi_internal.h"
+#include "minivllm_hip.h"
 
 namespace mgi {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTileKeys = 64;  // keys per LDS tile
@@ -39,6 +40,7 @@ template <> struct PF<bf16_t> {
   static constexpr int kKPad = 16;
   static constexpr int kVPad = 16;
 };
+template <> struct PF<f16_t> : PF<bf16_t> {};
 template <> struct PF<float> {
   static constexpr int kChunk = 4;
   static constexpr int kKPad = 4;
@@ -82,14 +84,40 @@ __device__ __forceinline__ KeyRows key_rows(const PrefillArgs& a, int key, int k
 // accumulators are rescaled on few tiles.
 constexpr float kRescaleSlack = 8.f;
 
-// Two bf16 values -> packed bf16x2 (hardware round to nearest even).
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
+// The 2-byte input types: a 16x16x32 MFMA on eight packed values per lane and
+// operand, and a two-value pack with the hardware conversion (round to
+// nearest even).
+template <typename T> struct Mma16;
+template <> struct Mma16<bf16_t> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  __device__ static __forceinline__ f32x4_t mfma(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c,
+                                                   0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    const v2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <> struct Mma16<f16_t> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  __device__ static __forceinline__ f32x4_t mfma(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c,
+                                                  0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    const v2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <> struct Mma16<float> {  // never called: fp32 takes the 16x16x4 path
+  __device__ static __forceinline__ f32x4_t mfma(uint4, uint4, f32x4_t c) { return c; }
+  __device__ static __forceinline__ uint32_t pack2(float, float) { return 0u; }
+};
 
-// Column of key k (0..63) in a bf16 V^T tile row. Keys 32c + 16h + 4g + i
+// Column of key k (0..63) in a 2-byte V^T tile row. Keys 32c + 16h + 4g + i
 // sit at 32c + 8g + 4h + i, so the eight keys one lane feeds to a PV MFMA
 // (4g+i and 16+4g+i of a 32-key slice) are one 16-byte LDS read.
 __device__ __forceinline__ int vt_col_bf16(int k) {
@@ -109,8 +137,9 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   constexpr int ITEMS = 16 * CPR;              // (4-key group, chunk) pairs per tile
   constexpr int IPT = (ITEMS + NT - 1) / NT;
   constexpr int QB = 16 * QPW * WAVES;         // query rows per workgroup
-  constexpr bool kBF16 = sizeof(T) == 2;
-  constexpr int NQF = kBF16 ? DP / 32 : DP / 16;   // Q fragments (16 bytes each)
+  constexpr bool k16 = sizeof(T) == 2;             // bf16 or f16
+  using MM = Mma16<T>;
+  constexpr int NQF = k16 ? DP / 32 : DP / 16;     // Q fragments (16 bytes each)
   constexpr int NDB = DP / 16;                     // 16-wide head-dim blocks of O^T
 
   // Two stages: tile t is read from one while tile t+1 is written to the other.
@@ -160,7 +189,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
                     (int64_t)h * a.q_sh;
 #pragma unroll
     for (int f = 0; f < NQF; ++f) {
-      const int d = kBF16 ? 32 * f + 8 * g : 16 * f + 4 * g;
+      const int d = k16 ? 32 * f + 8 * g : 16 * f + 4 * g;
       qf[b][f] = (ok && d < a.D) ? *reinterpret_cast<const uint4*>(qrow + d) : make_uint4(0, 0, 0, 0);
     }
   }
@@ -201,7 +230,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         *reinterpret_cast<uint4*>(&kl[(4 * kq_k + r) * KROW + dc_k * CH]) = kr[j][r];
-      if constexpr (kBF16) {
+      if constexpr (k16) {
         // 8 head dims x 4 keys -> eight 4-key runs of V^T rows. Each packed
         // pair takes the same 16-bit half of one word of two keys' rows
         // (v_perm_b32 byte select: 0-3 from the second operand, 4-7 from the first).
@@ -253,12 +282,10 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
       const T* krow = &kl[(16 * kb + col) * KROW];
 #pragma unroll
       for (int f = 0; f < NQF; ++f) {
-        if constexpr (kBF16) {
-          const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(krow + 32 * f + 8 * g));
+        if constexpr (k16) {
+          const uint4 kv = *reinterpret_cast<const uint4*>(krow + 32 * f + 8 * g);
 #pragma unroll
-          for (int b = 0; b < QPW; ++b)
-            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, __builtin_bit_cast(bf16x8_t, qf[b][f]),
-                                                               s[b][kb], 0, 0, 0);
+          for (int b = 0; b < QPW; ++b) s[b][kb] = MM::mfma(kv, qf[b][f], s[b][kb]);
         } else {
           const float4 kv = *reinterpret_cast<const float4*>(krow + 16 * f + 4 * g);
 #pragma unroll
@@ -342,25 +369,21 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     }
 
     // ---- O^T += V^T P^T
-    if constexpr (kBF16) {
+    if constexpr (k16) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        bf16x8_t pb[QPW];
+        uint4 pb[QPW];
 #pragma unroll
-        for (int b = 0; b < QPW; ++b) {
-          const uint4 w = make_uint4(pack_bf16x2(p[b][2 * c][0], p[b][2 * c][1]),
-                                     pack_bf16x2(p[b][2 * c][2], p[b][2 * c][3]),
-                                     pack_bf16x2(p[b][2 * c + 1][0], p[b][2 * c + 1][1]),
-                                     pack_bf16x2(p[b][2 * c + 1][2], p[b][2 * c + 1][3]));
-          pb[b] = __builtin_bit_cast(bf16x8_t, w);
-        }
+        for (int b = 0; b < QPW; ++b)
+          pb[b] = make_uint4(MM::pack2(p[b][2 * c][0], p[b][2 * c][1]),
+                             MM::pack2(p[b][2 * c][2], p[b][2 * c][3]),
+                             MM::pack2(p[b][2 * c + 1][0], p[b][2 * c + 1][1]),
+                             MM::pack2(p[b][2 * c + 1][2], p[b][2 * c + 1][3]));
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          const bf16x8_t va = __builtin_bit_cast(
-              bf16x8_t, *reinterpret_cast<const uint4*>(&vl[(16 * db + col) * VROW + 32 * c + 8 * g]));
+          const uint4 va = *reinterpret_cast<const uint4*>(&vl[(16 * db + col) * VROW + 32 * c + 8 * g]);
 #pragma unroll
-          for (int b = 0; b < QPW; ++b)
-            oacc[b][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[b], oacc[b][db], 0, 0, 0);
+          for (int b = 0; b < QPW; ++b) oacc[b][db] = MM::mfma(va, pb[b], oacc[b][db]);
         }
       }
     } else {
@@ -429,10 +452,10 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     for (int db = 0; db < NDB; ++db) {
       const int d0 = 16 * db + 4 * g;
       if (d0 >= a.D) continue;
-      if constexpr (kBF16) {
+      if constexpr (k16) {
         uint2 w;
-        w.x = pack_bf16x2(oacc[b][db][0] * inv, oacc[b][db][1] * inv);
-        w.y = pack_bf16x2(oacc[b][db][2] * inv, oacc[b][db][3] * inv);
+        w.x = MM::pack2(oacc[b][db][0] * inv, oacc[b][db][1] * inv);
+        w.y = MM::pack2(oacc[b][db][2] * inv, oacc[b][db][3] * inv);
         *reinterpret_cast<uint2*>(orow + d0) = w;
       } else {
         *reinterpret_cast<float4*>(orow + d0) = make_float4(oacc[b][db][0] * inv, oacc[b][db][1] * inv,
@@ -456,11 +479,11 @@ hipError_t launch_dp(const PrefillArgs& a, int waves, int qpw, hipStream_t strea
 
 }  // namespace
 
-int prefill_head_dim_bucket(int dtype_is_bf16, int D) {
+int prefill_head_dim_bucket(int two_byte, int D) {
   if (D <= 32) return 32;
   if (D <= 64) return 64;
   if (D <= 128) return 128;
-  if (dtype_is_bf16 && D <= 256) return 256;
+  if (two_byte && D <= 256) return 256;
   return 0;
 }
 
@@ -469,16 +492,23 @@ int prefill_head_dim_bucket(int dtype_is_bf16, int D) {
 // blocks per wavefront (which holds one wavefront per SIMD, so MFMA and
 // softmax work cannot overlap across wavefronts) and two- or eight-wavefront
 // workgroups, so only QPW == 1 is instantiated.
-hipError_t launch_paged_prefill(const PrefillArgs& a, bool bf16, int dp, int waves, int qpw,
+hipError_t launch_paged_prefill(const PrefillArgs& a, int dtype, int dp, int waves, int qpw,
                                 hipStream_t stream) {
-  if (bf16) {
+  if (dtype == MGI_BF16) {
     switch (dp) {
       case 32: return launch_dp<bf16_t, 32>(a, waves, qpw, stream);
       case 64: return launch_dp<bf16_t, 64>(a, waves, qpw, stream);
       case 128: return launch_dp<bf16_t, 128>(a, waves, qpw, stream);
       case 256: return launch_dp<bf16_t, 256>(a, waves, qpw, stream);
     }
-  } else {
+  } else if (dtype == MGI_F16) {
+    switch (dp) {
+      case 32: return launch_dp<f16_t, 32>(a, waves, qpw, stream);
+      case 64: return launch_dp<f16_t, 64>(a, waves, qpw, stream);
+      case 128: return launch_dp<f16_t, 128>(a, waves, qpw, stream);
+      case 256: return launch_dp<f16_t, 256>(a, waves, qpw, stream);
+    }
+  } else if (dtype == MGI_F32) {
     switch (dp) {
       case 32: return launch_dp<float, 32>(a, waves, 1, stream);
       case 64: return launch_dp<float, 64>(a, waves, 1, stream);

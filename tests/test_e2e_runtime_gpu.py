@@ -8,10 +8,10 @@ Comparison (as in experiments/gpu_day6_runtime_decode_ab.py:59-130):
   * scheduling is token-independent, so iterations, preemptions, repeated KV
     tokens and prefill/decode token counts must be identical;
   * fp32: decode logits within 2e-4 and greedy tokens identical;
-  * bf16: the reference backend accumulates in bf16 and the HIP kernels in
-    fp32, so tokens may only differ where the reference's top-2 logit margin
-    is a near tie (< 0.1); the first token (from prefill, shared by both
-    backends) must always agree.
+  * bf16 and f16: the reference backend accumulates in the 16-bit type and
+    the HIP kernels in fp32, so tokens may only differ where the reference's
+    top-2 logit margin is a near tie (< 0.1); the first token (from prefill,
+    shared by both backends) must always agree.
 """
 from __future__ import annotations
 
@@ -49,7 +49,7 @@ def run_capture(model, backend, prompts, dtype):
     return {s.seq_id: (len(s.prompt_tokens), list(s.generated_tokens)) for s in seqs}, captured, stats
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_runtime_with_preemption_hip_matches_reference(dtype):
     torch.backends.cuda.matmul.allow_tf32 = False
     prompts = _e2e.make_prompts(SPEC)

@@ -3,12 +3,13 @@
 Kernel level: every element against the prefill oracle, evaluated in double
 on the same inputs. Tolerances are those of the reference's prefix test
 (tests/test_prefill_prefix_sdpa_v2.py:58-63) for fp32 -- atol 2e-5, rtol 2e-4
--- and 2e-2 for bf16. Pools hold NaN in every slot no chunk row may see,
+-- 2e-2 for bf16 and 2e-3 for f16 (whose softmax weights and output round
+to 11 significant bits). Pools hold NaN in every slot no chunk row may see,
 tables are scattered permutations, and q is a strided view of a fused QKV
 row as in the model. Shapes cover the matrix-core buckets (head_dim 32, 64,
 128, 256), partial tiles, chunks after a long prefix, block sizes that are
-not powers of two, and the generic path (f16, head dims off the 16-byte
-grid, non-unit head-dim strides).
+not powers of two, and the generic path (head dims off the 16-byte grid,
+non-unit head-dim strides).
 
 Model level: the reference's prefix test recast for the "hip" prefill mode,
 the golden Mini-GPT token streams with HIP prefill and decode, and a bf16
@@ -36,6 +37,9 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 F32_TOL = dict(rtol=2e-4, atol=2e-5)
 BF16_TOL = dict(rtol=2e-2, atol=2e-2)
+F16_TOL = dict(rtol=2e-3, atol=2e-3)
+TOL = {torch.float32: F32_TOL, torch.bfloat16: BF16_TOL, torch.float16: F16_TOL}
+DTYPES = dict(argvalues=[torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 
 
 def prefill_case(start, T, H, D, S, dtype, seed=0, L=2, layer=1, spare=3):
@@ -73,8 +77,7 @@ def check(out, q, pool, table, start, layer):
                              table.numpy(), start, layer)
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()
-    tol = F32_TOL if q.dtype == torch.float32 else BF16_TOL
-    np.testing.assert_allclose(got, want, **tol)
+    np.testing.assert_allclose(got, want, **TOL[q.dtype])
 
 
 CASES = [
@@ -93,7 +96,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", **DTYPES)
 @pytest.mark.parametrize("start,T,H,D,S", CASES)
 def test_matches_oracle(start, T, H, D, S, dtype):
     qkv, pool, table, layer = prefill_case(start, T, H, D, S, dtype)
@@ -102,7 +105,7 @@ def test_matches_oracle(start, T, H, D, S, dtype):
     check(out, q, pool, table, start, layer)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", **DTYPES)
 def test_invalid_table_entries_are_masked(dtype):
     """Entries outside [0, N) mask their block's keys; a row with no visible key is zero."""
     qkv, pool, table, layer = prefill_case(40, 60, 4, 128, 16, dtype, seed=11)
@@ -127,9 +130,9 @@ def test_int32_table_and_contiguous_q_match_int64_and_view():
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-@pytest.mark.parametrize("dtype,D,strided", [(torch.float16, 64, False), (torch.bfloat16, 12, False),
+@pytest.mark.parametrize("dtype,D,strided", [(torch.float16, 20, False), (torch.bfloat16, 12, False),
                                              (torch.float32, 64, True)],
-                         ids=["f16", "bf16_d12", "f32_dstride2"])
+                         ids=["f16_d20", "bf16_d12", "f32_dstride2"])
 def test_generic_path(dtype, D, strided):
     start, T, H, S = 21, 30, 3, 16
     qkv, pool, table, layer = prefill_case(start, T, H, D, S, dtype, seed=5)
@@ -139,8 +142,7 @@ def test_generic_path(dtype, D, strided):
     out = run_hip(q, pool, table, start, layer)
     want = ora.paged_prefill(fx.to_numpy(q.float()), fx.to_numpy(pool.k.float()),
                              fx.to_numpy(pool.v.float()), table.numpy(), start, layer)
-    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
-    np.testing.assert_allclose(out.float().cpu().numpy(), want, **tol)
+    np.testing.assert_allclose(out.float().cpu().numpy(), want, **TOL[dtype])
 
 
 def test_one_row_chunk_equals_the_decode_kernel():
