@@ -452,7 +452,7 @@ def cpu_prefill_baseline(start: int = 0, T: int = 512, H: int = 16, D: int = 128
                       "oracle.paged_decode.paged_prefill in float32; median of 2 after 1 warmup"}
 
 
-def profiled_traffic(workload: str, split: int):
+def profiled_traffic(workload: str, split: dict):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     counter summary (FETCH_SIZE and WRITE_SIZE, each scaled by a copy kernel of
     known size), when profiles/ holds one for this workload and split."""
@@ -462,7 +462,7 @@ def profiled_traffic(workload: str, split: int):
                 d = json.loads(block)
             except json.JSONDecodeError:
                 continue
-            if d.get("workload") == workload and d.get("split_tokens") == split:
+            if d.get("workload") == workload and d.get("split") == split:
                 kib = d["fetch_kib_per_dispatch"] * d["fetch_scale"] + d["write_kib_per_dispatch"] * d["write_scale"]
                 return int(kib * 1024), md.name
     return None, None
@@ -500,8 +500,14 @@ def main() -> None:
         w = fx.make_decode_workload(B, H, D, S, N, 512, 4096, dtype, dev, seed=0, poison=False)
         from minivllm import _native
 
-        split = int(_native.lib().mgi_paged_decode_split_tokens(B, H, D, S, w.tables.shape[1],
-                                                                 args.split_tokens))
+        M = w.tables.shape[1]
+        bal = int(_native.lib().mgi_paged_decode_balanced_waves(B, H, D, S, M, args.split_tokens))
+        if bal:
+            split = {"mode": "balanced", "waves": bal * -(-H // 4)}  # 4 heads per wavefront at D=128
+        else:
+            split = {"mode": "partition",
+                     "split_tokens": int(_native.lib().mgi_paged_decode_split_tokens(B, H, D, S, M,
+                                                                                     args.split_tokens))}
         log("timing decode")
         main_line = decode_line(w, args.steps, args.warmup, args.split_tokens)
         log(f"decode: {main_line}")
@@ -615,7 +621,7 @@ def main() -> None:
         "data": "synthetic: seeded N(0,1) q/K/V, contexts and a random block permutation (seed 0)",
         "config": {"workload": "paged decode attention microbench (one layer, one decode step)",
                    "batch": B, "heads": H, "head_dim": D, "block_size": S, "pool_blocks": N,
-                   "ctx": "U[512,4096]", "sum_ctx": main_line["sum_ctx"], "split_tokens": split},
+                   "ctx": "U[512,4096]", "sum_ctx": main_line["sum_ctx"], "split": split},
         "pct_of_peak": main_line["pct_of_peak"],
         "decode_seq_per_s_per_layer": main_line["seq_per_s_per_layer"],
         "end_to_end": e2e_summary,
@@ -623,7 +629,8 @@ def main() -> None:
                      "frac": round(main_line["gbps"] / PEAK_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
                      "alg_bytes_per_launch": main_line["alg_bytes"],
-                     "kernel": "paged_decode_fast + paged_decode_merge (one mgi_paged_decode call)"},
+                     "kernel": ("paged_decode_fast_bal" if split["mode"] == "balanced" else "paged_decode_fast")
+                               + " + paged_decode_merge (one mgi_paged_decode call)"},
         "cpu_baseline": cpu,
         "extra": extras,
     }

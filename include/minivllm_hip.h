@@ -109,10 +109,14 @@ int mgi_kv_append(void* k_pool, void* v_pool,
  * online_v1 result for a row with no active block).
  * q, out and the pool share one dtype; arithmetic is fp32.
  *
- * split_tokens: tokens per context partition for the split-context pass
- * (0 = choose automatically; otherwise rounded to a multiple of S). Contexts
- * longer than one partition are processed as independent partitions whose
- * (max, sum, unnormalised output) partials are merged by a second pass.
+ * split_tokens: 0 lets the library split the work. When a table is wider
+ * than one partition and B <= 4096 it splits evenly: the blocks of all
+ * sequences, in sequence order, are dealt out in equal runs to a fixed
+ * number of wavefronts (mgi_paged_decode_balanced_waves), whatever the spread
+ * of context lengths. Otherwise, and for split_tokens > 0 (rounded to a
+ * multiple of S), each context is cut into partitions of split_tokens
+ * tokens. Either way, a sequence whose work is split writes (max, sum,
+ * unnormalised output) partials that a second pass merges.
  * workspace must hold mgi_paged_decode_workspace_bytes(...) bytes for the
  * same (B, H, D, S, M, split_tokens); it may be NULL when that is 0.
  */
@@ -136,10 +140,19 @@ size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D,
                                         int64_t S, int64_t M,
                                         int64_t split_tokens);
 
-/* The partition size (tokens) mgi_paged_decode uses for these sizes. */
+/* The partition size (tokens) mgi_paged_decode uses for these sizes when it
+ * splits contexts into partitions. */
 int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D,
                                       int64_t S, int64_t M,
                                       int64_t split_tokens);
+
+/* Wavefronts per group of heads of the even split mgi_paged_decode uses for
+ * these sizes on the current device, or 0 when it splits into partitions
+ * (or does not split). No counterpart in the reference: it reports the
+ * split, as mgi_paged_decode_split_tokens does. */
+int64_t mgi_paged_decode_balanced_waves(int64_t B, int64_t H, int64_t D,
+                                        int64_t S, int64_t M,
+                                        int64_t split_tokens);
 
 /*
  * Paged prefill attention of one chunk of one sequence.

@@ -76,20 +76,64 @@ int64_t split_tokens_for(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
   return std::min(P, max_ctx);
 }
 
-struct WorkspaceLayout {
-  size_t acc_bytes, ml_offset, total;
-  int64_t max_parts;
+// Balanced split of the fast kernel (paged_decode_fast_bal): every wave of a
+// head group streams the same number of blocks of the concatenated block
+// list of all sequences. Used when the partition split would cut some
+// contexts (more than one partition per table) and the caller left the split
+// to the library. The waves of all head groups together number three per
+// CU, so all of them are resident at once (the fast kernel's registers allow
+// one per SIMD) and finish together, each taking at least kBalMinTokens
+// tokens. Measured on MI355X (B=64 ragged, B=256, B=8 long contexts; bf16 and
+// f32): 2-3 waves per CU are best and within noise of each other; 4 per CU is
+// 1-2% slower, and 5-6 per CU (a partial second round) up to 10% slower.
+// MINIVLLM_HIP_DECODE_BALANCED=0 turns the mode off and MINIVLLM_HIP_BAL_WAVES
+// sets the total wave count (tuning).
+constexpr int64_t kBalMinTokens = 256;
+
+int env_int(const char* name, int dflt) {
+  const char* e = std::getenv(name);
+  return e ? std::atoi(e) : dflt;
+}
+
+struct SplitPlan {
+  int64_t P;             // partition mode: tokens per partition
+  int64_t max_parts;     // partials per (sequence, head)
+  int bal_waves;         // > 0: balanced mode, waves per head group
+  int bal_min_blocks;    // balanced mode: least blocks per wave
 };
 
-WorkspaceLayout workspace_layout(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
-                                 int64_t P) {
+SplitPlan split_plan(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M, int64_t requested) {
+  static const int balanced = env_int("MINIVLLM_HIP_DECODE_BALANCED", 1);
+  static const int waves = env_int("MINIVLLM_HIP_BAL_WAVES", 0);
+  SplitPlan sp{};
+  sp.P = split_tokens_for(B, H, D, S, M, requested);
+  sp.max_parts = (M * S + sp.P - 1) / sp.P;
+  if (balanced && requested <= 0 && sp.max_parts > 1 && B <= mgi::kBalMaxB &&
+      B * M < (int64_t(1) << 31)) {
+    const int64_t lph = D <= 32 ? 4 : D <= 64 ? 8 : D <= 128 ? 16 : 32;
+    const int64_t groups = (H + 64 / lph - 1) / (64 / lph);
+    const int64_t target = waves > 0 ? waves : 3 * (int64_t)device_cus();
+    sp.bal_waves = (int)std::max<int64_t>(1, target / groups);
+    sp.bal_min_blocks = (int)((kBalMinTokens + S - 1) / S);
+    sp.max_parts = (M + sp.bal_min_blocks - 1) / sp.bal_min_blocks + 1;
+  }
+  return sp;
+}
+
+struct WorkspaceLayout {
+  size_t acc_bytes, ml_offset, cinc_offset, total;
+};
+
+// [acc: B*H*max_parts*D f32 | ml: B*H*max_parts float2 | cinc: B int32
+// (balanced mode)], each part 256-byte aligned.
+WorkspaceLayout workspace_layout(int64_t B, int64_t H, int64_t D, const SplitPlan& sp) {
   WorkspaceLayout w{};
-  w.max_parts = (M * S + P - 1) / P;
-  if (w.max_parts <= 1) return w;
-  const int64_t n = B * H * w.max_parts;
+  if (sp.max_parts <= 1) return w;
+  const int64_t n = B * H * sp.max_parts;
   w.acc_bytes = (size_t)(n * D * 4);
   w.ml_offset = (size_t)round_up((int64_t)w.acc_bytes, kWorkspaceAlign);
-  w.total = w.ml_offset + (size_t)(n * 8);
+  w.cinc_offset = (size_t)round_up((int64_t)w.ml_offset + n * 8, kWorkspaceAlign);
+  w.total = sp.bal_waves > 0 ? w.cinc_offset + (size_t)(B * 4) : w.ml_offset + (size_t)(n * 8);
   return w;
 }
 
@@ -126,11 +170,16 @@ int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D, int64_t S
   return split_tokens_for(B, H, D, S, M, split_tokens);
 }
 
+int64_t mgi_paged_decode_balanced_waves(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
+                                        int64_t split_tokens) {
+  if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || M <= 0) return 0;
+  return split_plan(B, H, D, S, M, split_tokens).bal_waves;
+}
+
 size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                         int64_t split_tokens) {
   if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || M <= 0) return 0;
-  const int64_t P = split_tokens_for(B, H, D, S, M, split_tokens);
-  return workspace_layout(B, H, D, S, M, P).total;
+  return workspace_layout(B, H, D, split_plan(B, H, D, S, M, split_tokens)).total;
 }
 
 int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
@@ -168,8 +217,8 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   const char* kbase = static_cast<const char*>(k_pool) + layer_idx * k_pool_strides[0] * eb;
   const char* vbase = static_cast<const char*>(v_pool) + layer_idx * v_pool_strides[0] * eb;
 
-  const int64_t P = split_tokens_for(B, H, D, S, M, split_tokens);
-  const WorkspaceLayout ws = workspace_layout(B, H, D, S, M, P);
+  const SplitPlan sp = split_plan(B, H, D, S, M, split_tokens);
+  const WorkspaceLayout ws = workspace_layout(B, H, D, sp);
 
   // Path selection: the fast kernel needs unit d-stride, 16-byte aligned head
   // rows, head_dim a multiple of 8 up to 256 and S a multiple of its step.
@@ -235,8 +284,8 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   a.M = (int)M;
   a.N = N;
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.part_tokens = (int)P;
-  a.max_parts = plan.path == DecodePath::kFast ? (int)ws.max_parts : 1;
+  a.part_tokens = (int)sp.P;
+  a.max_parts = plan.path == DecodePath::kFast ? (int)sp.max_parts : 1;
   if (a.max_parts > 1) {
     if (!workspace) return fail(MGI_EWORKSPACE, "workspace required for split-context pass");
     if (workspace_bytes < ws.total)
@@ -244,6 +293,11 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
     if (!aligned16(workspace)) return fail(MGI_EINVAL, "workspace must be 16-byte aligned");
     a.ws_acc = static_cast<float*>(workspace);
     a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + ws.ml_offset);
+    if (sp.bal_waves > 0) {
+      a.bal_waves = sp.bal_waves;
+      a.bal_min_blocks = sp.bal_min_blocks;
+      a.ws_cinc = reinterpret_cast<int*>(static_cast<char*>(workspace) + ws.cinc_offset);
+    }
   }
 
   const hipError_t e = launch_paged_decode(a, dtype, plan, static_cast<hipStream_t>(stream));

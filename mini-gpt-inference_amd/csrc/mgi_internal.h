@@ -28,10 +28,13 @@ struct DecodeArgs {
   int B, H, D, S, M;
   int64_t N;
   float scale_log2;   // softmax scale * log2(e): scores live in the log2 domain
-  int part_tokens;    // tokens per context partition (multiple of S)
-  int max_parts;      // partitions per sequence covered by the grid
+  int part_tokens;    // partition mode: tokens per context partition (multiple of S)
+  int max_parts;      // partials per (sequence, head) the workspace holds
+  int bal_waves;      // > 0: balanced mode with this many waves per head group
+  int bal_min_blocks; // balanced mode: least blocks per wave
   float* ws_acc;      // [B, H, max_parts, D] unnormalised partial outputs
   float2* ws_ml;      // [B, H, max_parts]    partial (max, sum), log2 domain
+  int* ws_cinc;       // balanced mode: [B] inclusive prefix sums of blocks per sequence
 };
 
 // KV append / scatter. Pool pointers already point at layer layer_idx.
@@ -72,6 +75,10 @@ struct PrefillArgs {
   int64_t N;
   float scale_log2;   // softmax scale * log2(e)
 };
+
+// Largest batch of the fast decode kernel's balanced mode (its per-wave
+// prefix sums of blocks per sequence live in LDS).
+constexpr int kBalMaxB = 4096;
 
 enum class DecodePath { kFast, kGeneric };
 

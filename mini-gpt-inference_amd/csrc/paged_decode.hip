@@ -145,9 +145,8 @@ __device__ __forceinline__ void store_out(const DecodeArgs& a, int b, int h, int
 
 // ------------------------------------------------------------- fast kernel
 
-// Largest number of S-token blocks one partition may span: the partition's
-// block-table entries are held one per lane in two VGPRs (the host caps the
-// partition size at kMaxBlocksPerPart * S).
+// Largest number of S-token blocks one chunk of a wave's work may span: the
+// chunk's block-table entries are held one per lane in two VGPRs.
 constexpr int kMaxBlocksPerPart = 128;
 
 // Raw K and V fragments of TOK consecutive tokens of one block.
@@ -157,139 +156,137 @@ struct Step {
   uint4 v[TOK][Layout<T>::kLoads];
 };
 
-template <typename T, int LPH, int TOK, bool FULL>
-__global__ void __launch_bounds__(64)
-paged_decode_fast(const DecodeArgs a) {
-  constexpr int HPW = 64 / LPH;
-  constexpr int NL = Layout<T>::kLoads;
+// Byte offsets of this lane's loads inside one token row of the pool.
+template <typename T>
+__device__ __forceinline__ void row_offsets(const DecodeArgs& a, int h, int sub, bool lane_ok,
+                                            uint32_t (&koff)[Layout<T>::kLoads],
+                                            uint32_t (&voff)[Layout<T>::kLoads]) {
   constexpr int EB = (int)sizeof(T);
-  const int lane = (int)threadIdx.x;
-  const int sub = lane % LPH;
-  const int row = lane / LPH;
-  const int b = (int)blockIdx.z;
-  const int part = (int)blockIdx.y;
-  const int h = (int)blockIdx.x * HPW + row;
-  const int D = a.D;
-  const int S = a.S;
-  const bool lane_ok = FULL || (h < a.H && sub * 8 < D);
-
-  const int ctx = clamp_ctx<T>(a, b);
-  const int P = a.part_tokens;
-  const int nparts = (ctx + P - 1) / P;
-  if (part >= (nparts > 0 ? nparts : 1)) return;  // uniform over the wave
-
-  const int t_begin = part * P;  // a multiple of S
-  const int t_end = min(ctx, t_begin + P);
-  const int nsteps = (t_end - t_begin + TOK - 1) / TOK;
-  const int blk0 = t_begin / S;
-  const int nblk = (t_end - t_begin + S - 1) / S;  // <= kMaxBlocksPerPart
-
-  // Lane j holds this partition's physical block ids j (phys_lo) and 64 + j
-  // (phys_hi); -1 marks an out-of-range entry (masked) or no block.
-  int phys_lo = -1, phys_hi = -1;
-  const int64_t bt_row = (int64_t)b * a.bt_sb;
-  if (lane < nblk) {
-    const int64_t e = load_index(a.bt, a.bt_i64, bt_row + (int64_t)(blk0 + lane) * a.bt_sm);
-    phys_lo = (e >= 0 && e < a.N) ? (int)e : -1;
+#pragma unroll
+  for (int j = 0; j < Layout<T>::kLoads; ++j) {
+    koff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.k_sh + Layout<T>::load_off(sub, a.D, j)) * EB) : 0u;
+    voff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.v_sh + Layout<T>::load_off(sub, a.D, j)) * EB) : 0u;
   }
-  if (64 + lane < nblk) {
-    const int64_t e = load_index(a.bt, a.bt_i64, bt_row + (int64_t)(blk0 + 64 + lane) * a.bt_sm);
-    phys_hi = (e >= 0 && e < a.N) ? (int)e : -1;
-  }
+}
 
-  QFrag<T> q;
+template <typename T>
+__device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h, int sub, bool lane_ok,
+                                           QFrag<T>& q) {
   q.zero();
   if (lane_ok)
-    q.load(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh,
-           a.q_sd, sub, D);
+    q.load(reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh, a.q_sd, sub,
+           a.D);
+}
 
-  // Byte offsets of this lane's loads inside one token row of the pool.
-  uint32_t koff[NL], voff[NL];
-#pragma unroll
-  for (int j = 0; j < NL; ++j) {
-    koff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.k_sh + Layout<T>::load_off(sub, D, j)) * EB) : 0u;
-    voff[j] = lane_ok ? (uint32_t)(((int64_t)h * a.v_sh + Layout<T>::load_off(sub, D, j)) * EB) : 0u;
-  }
+// Folds the tokens of blocks [blk_begin, blk_end) of sequence b, clipped to
+// its context ctx, into the wave's online-softmax state (m, l, acc); the
+// chunk spans at most kMaxBlocksPerPart blocks. Scores live in the log2
+// domain.
+template <typename T, int LPH, int TOK, bool FULL>
+__device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane, bool lane_ok,
+                                            const QFrag<T>& q,
+                                            const uint32_t (&koff)[Layout<T>::kLoads],
+                                            const uint32_t (&voff)[Layout<T>::kLoads],
+                                            int blk_begin, int blk_end, int ctx, float& m, float& l,
+                                            float (&acc)[8]) {
+  constexpr int NL = Layout<T>::kLoads;
+  constexpr int EB = (int)sizeof(T);
+  const int S = a.S;
   const char* kl = reinterpret_cast<const char*>(a.k);
   const char* vl = reinterpret_cast<const char*>(a.v);
   const int64_t k_row = a.k_ss * EB, v_row = a.v_ss * EB;
   const int steps_per_blk = S / TOK;
+  const int64_t bt_row = (int64_t)b * a.bt_sb;
 
-  // Issues the K/V loads of step s (clamped to the last step: a step past the
-  // partition re-reads that step's lines, which are cache-resident, so every
-  // iteration issues the same number of loads). Returns the number of valid
-  // tokens of step s (0 past the partition or for a masked block).
-  auto issue = [&](int s, Step<T, TOK>& st) -> int {
-    const int sc = s < nsteps ? s : nsteps - 1;
-    const int rel = sc / steps_per_blk;
-    const int off = (sc - rel * steps_per_blk) * TOK;
-    const int phys = rel < 64 ? __builtin_amdgcn_readlane(phys_lo, rel)
-                              : __builtin_amdgcn_readlane(phys_hi, rel - 64);
-    const int nvalid = min(TOK, t_end - (t_begin + sc * TOK));
-    const int64_t pb = phys >= 0 ? phys : 0;  // a masked block is read from block 0, never used
-    const auto krs = make_rsrc(kl + (pb * a.k_sn + (int64_t)off * a.k_ss) * EB);
-    const auto vrs = make_rsrc(vl + (pb * a.v_sn + (int64_t)off * a.v_ss) * EB);
-    // Tokens past the context re-read the last valid token (never a slot
-    // past the context) and are masked out of the softmax.
-#pragma unroll
-    for (int t = 0; t < TOK; ++t) {
-      const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * k_row);
-#pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        if (FULL || lane_ok) st.k[t][j] = buffer_load16(krs, koff[j], so);
-        else st.k[t][j] = make_uint4(0u, 0u, 0u, 0u);
-      }
+  {
+    const int c0 = blk_begin;
+    const int t_begin = c0 * S;  // a multiple of S
+    const int t_end = min(ctx, blk_end * S);
+    if (t_end <= t_begin) return;  // uniform over the wave
+    const int nsteps = (t_end - t_begin + TOK - 1) / TOK;
+    const int nblk = (t_end - t_begin + S - 1) / S;  // <= kMaxBlocksPerPart
+
+    // Lane j holds the chunk's physical block ids j (phys_lo) and 64 + j
+    // (phys_hi); -1 marks an out-of-range entry (masked) or no block.
+    int phys_lo = -1, phys_hi = -1;
+    if (lane < nblk) {
+      const int64_t e = load_index(a.bt, a.bt_i64, bt_row + (int64_t)(c0 + lane) * a.bt_sm);
+      phys_lo = (e >= 0 && e < a.N) ? (int)e : -1;
     }
-#pragma unroll
-    for (int t = 0; t < TOK; ++t) {
-      const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * v_row);
-#pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        if (FULL || lane_ok) st.v[t][j] = buffer_load16(vrs, voff[j], so);
-        else st.v[t][j] = make_uint4(0u, 0u, 0u, 0u);
-      }
+    if (64 + lane < nblk) {
+      const int64_t e = load_index(a.bt, a.bt_i64, bt_row + (int64_t)(c0 + 64 + lane) * a.bt_sm);
+      phys_hi = (e >= 0 && e < a.N) ? (int)e : -1;
     }
-    return (s < nsteps && phys >= 0) ? nvalid : 0;
-  };
 
-  float m = -INFINITY, l = 0.f;
-  float acc[8];
+    // Issues the K/V loads of step s (clamped to the last step: a step past
+    // the chunk re-reads that step's lines, which are cache-resident, so every
+    // iteration issues the same number of loads). Returns the number of valid
+    // tokens of step s (0 past the chunk or for a masked block).
+    auto issue = [&](int s, Step<T, TOK>& st) -> int {
+      const int sc = s < nsteps ? s : nsteps - 1;
+      const int rel = sc / steps_per_blk;
+      const int off = (sc - rel * steps_per_blk) * TOK;
+      const int phys = rel < 64 ? __builtin_amdgcn_readlane(phys_lo, rel)
+                                : __builtin_amdgcn_readlane(phys_hi, rel - 64);
+      const int nvalid = min(TOK, t_end - (t_begin + sc * TOK));
+      const int64_t pb = phys >= 0 ? phys : 0;  // a masked block is read from block 0, never used
+      const auto krs = make_rsrc(kl + (pb * a.k_sn + (int64_t)off * a.k_ss) * EB);
+      const auto vrs = make_rsrc(vl + (pb * a.v_sn + (int64_t)off * a.v_ss) * EB);
+      // Tokens past the context re-read the last valid token (never a slot
+      // past the context) and are masked out of the softmax.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+      for (int t = 0; t < TOK; ++t) {
+        const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * k_row);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          if (FULL || lane_ok) st.k[t][j] = buffer_load16(krs, koff[j], so);
+          else st.k[t][j] = make_uint4(0u, 0u, 0u, 0u);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TOK; ++t) {
+        const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * v_row);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+          if (FULL || lane_ok) st.v[t][j] = buffer_load16(vrs, voff[j], so);
+          else st.v[t][j] = make_uint4(0u, 0u, 0u, 0u);
+        }
+      }
+      return (s < nsteps && phys >= 0) ? nvalid : 0;
+    };
 
-  // Folds one step into the online softmax (scores in the log2 domain).
-  auto consume = [&](const Step<T, TOK>& st, int nvalid) {
-    // No implicit FMA contraction: a score and the running max derived from
-    // it must be the same rounded value, so the largest score's weight is
-    // exactly 2^0 = 1 (explicit fmaf / dot2 calls are unaffected).
+    // Folds one step into the online softmax.
+    auto consume = [&](const Step<T, TOK>& st, int nvalid) {
+      // No implicit FMA contraction: a score and the running max derived from
+      // it must be the same rounded value, so the largest score's weight is
+      // exactly 2^0 = 1 (explicit fmaf / dot2 calls are unaffected).
 #pragma clang fp contract(off)
-    float s[TOK];
-    float mb = -INFINITY;
+      float s[TOK];
+      float mb = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < TOK; ++t) {
-      const float d = group_sum<LPH>(q.dot(st.k[t])) * a.scale_log2;
-      s[t] = t < nvalid ? d : -INFINITY;
-      mb = fmaxf(mb, s[t]);
-    }
-    const float mn = fmaxf(m, mb);
-    const float alpha = fast_exp2(m - mn);
-    float psum = 0.f;
+      for (int t = 0; t < TOK; ++t) {
+        const float d = group_sum<LPH>(q.dot(st.k[t])) * a.scale_log2;
+        s[t] = t < nvalid ? d : -INFINITY;
+        mb = fmaxf(mb, s[t]);
+      }
+      const float mn = fmaxf(m, mb);
+      const float alpha = fast_exp2(m - mn);
+      float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
 #pragma unroll
-    for (int t = 0; t < TOK; ++t) {
-      const float p = fast_exp2(s[t] - mn);
-      psum += p;
+      for (int t = 0; t < TOK; ++t) {
+        const float p = fast_exp2(s[t] - mn);
+        psum += p;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, frag_elem<T>(st.v[t], i), acc[i]);
-    }
-    l = l * alpha + psum;
-    m = mn;
-  };
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, frag_elem<T>(st.v[t], i), acc[i]);
+      }
+      l = l * alpha + psum;
+      m = mn;
+    };
 
-  // Two-deep software pipeline: the loads of step s+1 are in flight while
-  // step s is folded in.
-  if (nsteps > 0) {
+    // Two-deep software pipeline: the loads of step s+1 are in flight while
+    // step s is folded in.
     Step<T, TOK> A, B;
     int nva = issue(0, A);
     for (int s = 0; s < nsteps; s += 2) {
@@ -301,33 +298,190 @@ paged_decode_fast(const DecodeArgs a) {
       if (nvb > 0) consume(B, nvb);
     }
   }
+}
 
-  if (!lane_ok) return;  // no cross-lane work below
-  if (nparts <= 1) {
+// Writes a wave's state: the normalised output when the sequence has one
+// piece of work, else partial j of (b, h).
+template <typename T>
+__device__ __forceinline__ void finish_piece(const DecodeArgs& a, int b, int h, int sub, bool lane_ok,
+                                             float m, float l, const float (&acc)[8], int npieces,
+                                             int j) {
+  if (!lane_ok) return;
+  if (npieces <= 1) {
     store_out<T>(a, b, h, sub, acc, l > 0.f ? 1.f / l : 0.f);
     return;
   }
-  const size_t pidx = ((size_t)b * a.H + h) * a.max_parts + part;
-  float* wa = a.ws_acc + pidx * D;
-  float4* w0 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, D, 0));
-  float4* w1 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, D, 4));
+  const size_t pidx = ((size_t)b * a.H + h) * a.max_parts + j;
+  float* wa = a.ws_acc + pidx * a.D;
+  float4* w0 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, a.D, 0));
+  float4* w1 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, a.D, 4));
   *w0 = make_float4(acc[0], acc[1], acc[2], acc[3]);
   *w1 = make_float4(acc[4], acc[5], acc[6], acc[7]);
   if (sub == 0) a.ws_ml[pidx] = make_float2(m, l);
 }
 
-// Combines the partition partials of every (b, h) whose context spans more
-// than one partition. One wavefront per (sequence, HPW heads), the fast
-// kernel's head grouping: in each head row, lane j loads the (max, sum) of
-// partition p0 + j while every lane loads its 8 elements of all CH partial
-// outputs of the chunk, so a chunk costs one round trip; chunks fold online:
+// Partition mode: one wavefront per (HPW heads, partition of part_tokens
+// tokens, sequence); partitions past a context exit at once.
+template <typename T, int LPH, int TOK, bool FULL>
+__global__ void __launch_bounds__(64)
+paged_decode_fast(const DecodeArgs a) {
+  constexpr int HPW = 64 / LPH;
+  const int lane = (int)threadIdx.x;
+  const int sub = lane % LPH;
+  const int h = (int)blockIdx.x * HPW + lane / LPH;
+  const int part = (int)blockIdx.y;
+  const int b = (int)blockIdx.z;
+  const bool lane_ok = FULL || (h < a.H && sub * 8 < a.D);
+
+  const int ctx = clamp_ctx<T>(a, b);
+  const int P = a.part_tokens;
+  const int nparts = (ctx + P - 1) / P;
+  if (part >= (nparts > 0 ? nparts : 1)) return;  // uniform over the wave
+
+  QFrag<T> q;
+  load_query<T>(a, b, h, sub, lane_ok, q);
+  uint32_t koff[Layout<T>::kLoads], voff[Layout<T>::kLoads];
+  row_offsets<T>(a, h, sub, lane_ok, koff, voff);
+  float m = -INFINITY, l = 0.f, acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  const int bpp = P / a.S;  // P is a multiple of S
+  fold_chunk<T, LPH, TOK, FULL>(a, b, lane, lane_ok, q, koff, voff, part * bpp, (part + 1) * bpp, ctx,
+                                 m, l, acc);
+  finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, nparts, part);
+}
+
+// Balanced mode. The blocks of all sequences, in sequence order, form one
+// list of total = sum_b ceil(ctx_b / S) blocks. Wave w of each head group
+// takes the blocks [w*Wb, (w+1)*Wb) of that list, Wb = max(bal_min_blocks,
+// ceil(total / bal_waves)), so every wave streams the same number of blocks
+// whatever the spread of context lengths, and no wave is left running alone
+// at the end of the grid. A sequence split over several waves gets one
+// partial per wave (index w - floor(cb / Wb), cb its first block in the list),
+// combined by paged_decode_merge; a sequence inside one wave is written
+// directly.
+
+__device__ __forceinline__ int bal_blocks_per_wave(int total, int waves, int min_blocks) {
+  const int wb = (total + waves - 1) / waves;
+  return wb > min_blocks ? wb : min_blocks;
+}
+
+// Inclusive prefix sums of ceil(ctx_b / S) into cinc[0 .. B); returns the
+// total (uniform). One wavefront: lane i covers sequences [i*K, i*K + K).
+template <typename T>
+__device__ __forceinline__ int seq_block_scan(const DecodeArgs& a, int lane, int* cinc) {
+  const int K = (a.B + 63) / 64;
+  const int b0 = lane * K;
+  int sum = 0;
+  for (int k = 0; k < K; ++k) {
+    const int b = b0 + k;
+    if (b < a.B) sum += (clamp_ctx<T>(a, b) + a.S - 1) / a.S;
+  }
+  int incl = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  int run = incl - sum;
+  for (int k = 0; k < K; ++k) {
+    const int b = b0 + k;
+    if (b < a.B) {
+      run += (clamp_ctx<T>(a, b) + a.S - 1) / a.S;
+      cinc[b] = run;
+    }
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));
+}
+
+// Wave-uniform read of cinc[i] (i uniform): kept in a scalar register so the
+// buffer descriptors derived from it need no per-lane loops.
+__device__ __forceinline__ int uread(const int* cinc, int i) {
+  return __builtin_amdgcn_readfirstlane(cinc[i]);
+}
+
+template <typename T, int LPH, int TOK, bool FULL>
+__global__ void __launch_bounds__(64)
+paged_decode_fast_bal(const DecodeArgs a) {
+  constexpr int HPW = 64 / LPH;
+  __shared__ int cinc[kBalMaxB];
+  const int lane = (int)threadIdx.x;
+  const int sub = lane % LPH;
+  const int ngroups = (a.H + HPW - 1) / HPW;
+  const int hg = (int)blockIdx.x % ngroups;
+  const int w = (int)blockIdx.x / ngroups;
+  const int h = hg * HPW + lane / LPH;
+  const bool lane_ok = FULL || (h < a.H && sub * 8 < a.D);
+
+  const int total = seq_block_scan<T>(a, lane, cinc);
+  if (blockIdx.x == 0)  // the merge reads the block list from the workspace
+    for (int i = lane; i < a.B; i += 64) a.ws_cinc[i] = cinc[i];
+  const int wb = bal_blocks_per_wave(total, a.bal_waves, a.bal_min_blocks);
+  const int64_t first = (int64_t)w * wb;
+  if (first >= total) return;  // uniform over the wave
+  int pos = (int)first;
+  const int end = (int)min((int64_t)total, first + wb);
+
+  // The sequence holding list block pos: the first b with cinc[b] > pos.
+  int b = 0;
+  for (int lo = 0, hi = a.B - 1; lo <= hi;) {
+    const int mid = (lo + hi) >> 1;
+    if (uread(cinc, mid) > pos) {
+      b = mid;
+      hi = mid - 1;
+    } else {
+      lo = mid + 1;
+    }
+  }
+
+  uint32_t koff[Layout<T>::kLoads], voff[Layout<T>::kLoads];
+  row_offsets<T>(a, h, sub, lane_ok, koff, voff);
+  // One flat loop over chunks of at most kMaxBlocksPerPart blocks of one
+  // sequence; the state is written out when the wave leaves a sequence.
+  int cb = 0, ce = 0, ctx = 0;
+  QFrag<T> q;
+  float m = -INFINITY, l = 0.f, acc[8];
+  while (pos < end) {
+    if (pos >= ce) {  // entering sequence b
+      cb = b > 0 ? uread(cinc, b - 1) : 0;
+      ce = uread(cinc, b);
+      ctx = clamp_ctx<T>(a, b);
+      load_query<T>(a, b, h, sub, lane_ok, q);
+      m = -INFINITY;
+      l = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    }
+    const int ch_end = min(min(end, ce), pos + kMaxBlocksPerPart);
+    fold_chunk<T, LPH, TOK, FULL>(a, b, lane, lane_ok, q, koff, voff, pos - cb, ch_end - cb, ctx, m, l,
+                                  acc);
+    pos = ch_end;
+    if (pos == ce || pos == end) {
+      const int w_first = cb / wb;
+      finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, (ce - 1) / wb - w_first + 1, w - w_first);
+      // Next sequence with blocks past pos (cinc[B-1] = total bounds b while pos < end).
+      while (pos < end && uread(cinc, b) <= pos) ++b;
+    }
+  }
+}
+
+// Combines the partials of every (b, h) whose context spans more than one
+// piece of work (partition mode: ceil(ctx / part_tokens) partitions;
+// balanced mode: the waves its blocks fall in). One wavefront per (sequence,
+// HPW heads), the fast kernel's head grouping: in each head row, lane j loads
+// the (max, sum) of partial p0 + j while every lane loads its 8 elements of
+// all CH partial outputs of the chunk, so a chunk costs one round trip;
+// chunks fold online:
 //   M' = max(M, max_j m_j), L' = L 2^(M-M') + sum_j l_j 2^(m_j-M'),
 //   O' = O 2^(M-M') + sum_j O_j 2^(m_j-M').
+// In balanced mode it also writes the zero output of a sequence with no
+// blocks, which no attention wave visits.
 template <typename T, int LPH>
 __global__ void __launch_bounds__(64)
 paged_decode_merge(const DecodeArgs a) {
   constexpr int HPW = 64 / LPH;
-  constexpr int CH = LPH < 16 ? LPH : 16;  // partitions per chunk
+  constexpr int CH = LPH < 16 ? LPH : 16;  // partials per chunk
   const int lane = (int)threadIdx.x;
   const int sub = lane % LPH;
   const int row = lane / LPH;
@@ -336,15 +490,28 @@ paged_decode_merge(const DecodeArgs a) {
   const int D = a.D;
   const bool head_ok = h < a.H;
   const bool lane_ok = head_ok && sub * 8 < D;
-  const int ctx = clamp_ctx<T>(a, b);
-  const int nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  int nparts;
+  if (a.bal_waves > 0) {
+    const int total = a.ws_cinc[a.B - 1];
+    const int cb = b > 0 ? a.ws_cinc[b - 1] : 0;
+    const int ce = a.ws_cinc[b];
+    if (ce <= cb) {  // no blocks: zeros, as for an empty context
+      if (lane_ok) store_out<T>(a, b, h, sub, acc, 0.f);
+      return;
+    }
+    const int wb = bal_blocks_per_wave(total, a.bal_waves, a.bal_min_blocks);
+    nparts = (ce - 1) / wb - cb / wb + 1;
+  } else {
+    const int ctx = clamp_ctx<T>(a, b);
+    nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
+  }
   if (nparts <= 1) return;  // uniform over the wave
   const size_t base = ((size_t)b * a.H + (head_ok ? h : 0)) * a.max_parts;
 
   float M = -INFINITY, L = 0.f;
-  float acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   for (int p0 = 0; p0 < nparts; p0 += CH) {
     float2 ml = make_float2(-INFINITY, 0.f);
     if (head_ok && sub < CH && p0 + sub < nparts) ml = a.ws_ml[base + p0 + sub];
@@ -367,7 +534,7 @@ paged_decode_merge(const DecodeArgs a) {
     for (int i = 0; i < 8; ++i) acc[i] *= alpha;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const float wj = __shfl(w, row * LPH + j, 64);  // weight of partition p0 + j
+      const float wj = __shfl(w, row * LPH + j, 64);  // weight of partial p0 + j
       acc[0] = fmaf(wj, x0[j].x, acc[0]);
       acc[1] = fmaf(wj, x0[j].y, acc[1]);
       acc[2] = fmaf(wj, x0[j].z, acc[2]);
@@ -460,13 +627,20 @@ static hipError_t launch(const void* fn, dim3 grid, dim3 block, const DecodeArgs
 template <typename T, int LPH, int TOK>
 static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_t stream) {
   constexpr int HPW = 64 / LPH;
-  const dim3 grid((unsigned)((a.H + HPW - 1) / HPW), (unsigned)a.max_parts, (unsigned)a.B);
-  const void* fn = full ? reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, true>)
-                        : reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, false>);
-  hipError_t e = launch(fn, grid, dim3(64), a, stream);
+  const unsigned ngroups = (unsigned)((a.H + HPW - 1) / HPW);
+  hipError_t e;
+  if (a.bal_waves > 0) {
+    const void* fn = full ? reinterpret_cast<const void*>(&paged_decode_fast_bal<T, LPH, TOK, true>)
+                          : reinterpret_cast<const void*>(&paged_decode_fast_bal<T, LPH, TOK, false>);
+    e = launch(fn, dim3(ngroups * (unsigned)a.bal_waves), dim3(64), a, stream);
+  } else {
+    const void* fn = full ? reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, true>)
+                          : reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, false>);
+    e = launch(fn, dim3(ngroups, (unsigned)a.max_parts, (unsigned)a.B), dim3(64), a, stream);
+  }
   if (e != hipSuccess || a.max_parts <= 1) return e;
-  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH>),
-                dim3((unsigned)((a.H + HPW - 1) / HPW), (unsigned)a.B), dim3(64), a, stream);
+  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH>), dim3(ngroups, (unsigned)a.B),
+                dim3(64), a, stream);
 }
 
 template <typename T, int LPH>

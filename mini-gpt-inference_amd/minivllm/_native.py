@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "mgi_paged_decode",
     "mgi_paged_decode_workspace_bytes",
     "mgi_paged_decode_split_tokens",
+    "mgi_paged_decode_balanced_waves",
     "mgi_paged_prefill",
 )
 
@@ -75,6 +76,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mgi_paged_decode_workspace_bytes.argtypes = [_i64] * 6
     lib.mgi_paged_decode_split_tokens.restype = _i64
     lib.mgi_paged_decode_split_tokens.argtypes = [_i64] * 6
+    lib.mgi_paged_decode_balanced_waves.restype = _i64
+    lib.mgi_paged_decode_balanced_waves.argtypes = [_i64] * 6
     lib.mgi_paged_prefill.restype = _i
     lib.mgi_paged_prefill.argtypes = [
         _p, _pi64,                         # out, strides

@@ -35,10 +35,12 @@ def test_library_exports_every_declared_symbol():
 def test_split_tokens_and_workspace_sizes():
     lib = _native.lib()
     # decode microbench shape: M = 256 columns of S = 16 -> 8 partitions of 512
+    # (partition mode; the automatic split's workspace is checked in
+    # test_balanced_split.py)
     assert lib.mgi_paged_decode_split_tokens(64, 32, 128, 16, 256, 0) == 512
     n = 64 * 32 * 8
     acc = n * 128 * 4
-    assert lib.mgi_paged_decode_workspace_bytes(64, 32, 128, 16, 256, 0) == ((acc + 255) // 256) * 256 + n * 8
+    assert lib.mgi_paged_decode_workspace_bytes(64, 32, 128, 16, 256, 512) == ((acc + 255) // 256) * 256 + n * 8
     # a table that fits one partition needs no workspace
     assert lib.mgi_paged_decode_workspace_bytes(4, 8, 32, 16, 4, 0) == 0
     for S, M, req in [(16, 8192, 0), (8, 100, 0), (12, 77, 100), (16, 256, 1), (16, 256, 5000),

@@ -228,6 +228,28 @@ def test_decode_microbench_invariances():
     assert torch.equal(again.view(torch.int32), base.view(torch.int32))
 
 
+@pytest.mark.parametrize("B", [7, 200])
+def test_balanced_split_with_empty_and_one_token_contexts(B):
+    """The automatic split spreads every sequence's blocks evenly over the
+    waves (several sequences per wave, several waves per sequence); rows with
+    no context are zeros and one-token rows return their value row."""
+    S, H, D, M = 16, 4, 64, 80
+    g = torch.Generator().manual_seed(B)
+    choices = torch.tensor([0, 1, 2, 15, 16, 17, 300, 1000, M * S])
+    ctx = choices[torch.randint(len(choices), (B,), generator=g)]
+    ctx[0], ctx[-1] = 0, M * S
+    N = int(((ctx + S - 1) // S).sum()) + 8
+    print(f"  balanced split B={B} N={N}", flush=True)
+    q, pool, tables, lens, layer = _small_case(B, H, D, S, ctx.tolist(), torch.float32, seed=B, N=N)
+    assert tables.shape[1] <= M
+    tables = torch.nn.functional.pad(tables, (0, M - tables.shape[1]), value=-1)
+    assert hpd._native.lib().mgi_paged_decode_workspace_bytes(B, H, D, S, M, 0) > 0
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
+    want = c_oracle.paged_decode(*oracle_args(q, pool, tables, lens, layer))
+    np.testing.assert_allclose(got, want, **F32_TOL)
+    assert (got[ctx.numpy() == 0] == 0).all()
+
+
 def test_long_context_split_decode():
     """B=8, H=32, D=128, bf16, ctx ~ U[32768, 131072] over a 65536-block pool."""
     print("  workload B=8 ctx U[32768,131072] N=65536 bf16", flush=True)
