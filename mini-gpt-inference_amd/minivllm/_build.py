@@ -34,6 +34,11 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
+# Matrix-core accumulators in ordinary VGPRs: without this the compiler keeps
+# the prefill kernel's MFMA results in AGPRs and copies them back and forth
+# for the softmax (64 v_accvgpr moves per key tile).
+MFMA_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+MFMA_SOURCES = {"paged_prefill.hip"}
 
 
 def library_path() -> Path:
@@ -76,7 +81,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = OBJ_DIR / (src.stem + ".o")
-        _run([hipcc, *HIP_FLAGS, *includes, "-c", str(src), "-o", str(obj)], verbose)
+        extra = MFMA_FLAGS if src.name in MFMA_SOURCES else []
+        _run([hipcc, *HIP_FLAGS, *extra, *includes, "-c", str(src), "-o", str(obj)], verbose)
         return obj
 
     workers = jobs or min(len(sources), max(1, (os.cpu_count() or 2)))
