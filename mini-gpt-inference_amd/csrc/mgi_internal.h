@@ -74,6 +74,8 @@ struct PrefillArgs {
   int s_shift;        // log2(S) when S is a power of two, else -1
   int64_t N;
   float scale_log2;   // softmax scale * log2(e)
+  int pair_round;     // > 0: workgroups per XCD in one slot round (see the kernel's grid mapping)
+  int cus;            // compute units of the device (set by the caller)
 };
 
 // Largest batch of the fast decode kernel's balanced mode (its per-wave

@@ -151,12 +151,21 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   // 1-D grid of nq * H workgroups, dispatched round-robin over the XCDs
   // (workgroup id mod 8). With H a multiple of 8, every query tile of head h
   // runs on XCD h mod 8, so each XCD's L2 holds the K/V of H/8 heads only.
-  // Within a head, the longest (latest) query tiles go first.
+  // Within a head, the longest (latest) query tiles go first. When the whole
+  // grid is resident at once (two workgroups per CU, pair_round = CUs per
+  // XCD), the second round of an XCD's workgroups runs in the opposite
+  // order, so the two workgroups that share a CU have query tiles qt and
+  // nq-1-qt and about the same causal work together.
   const int nq = (a.T + QB - 1) / QB;
   const int wg = (int)blockIdx.x;
   int h, qr;
   if ((a.H & 7) == 0) {
-    const int j = wg >> 3;
+    int j = wg >> 3;
+    if (a.pair_round > 0 && (j / a.pair_round) & 1) {
+      const int lo = j - j % a.pair_round;
+      const int hi = min(lo + a.pair_round, (a.H >> 3) * nq);
+      j = hi - 1 - (j - lo);
+    }
     h = (wg & 7) + 8 * (j / nq);
     qr = j % nq;
   } else {
@@ -465,16 +474,35 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   }
 }
 
+// Workgroups of kernel `fn` (threads each) resident per CU at once.
+static int resident_per_cu(const void* fn, int threads) {
+  int n = 0;
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) == hipSuccess ? n : 0;
+}
+
+template <typename T, int DP, int WAVES>
+hipError_t launch_waves(const PrefillArgs& a, hipStream_t stream) {
+  constexpr int QB = 16 * WAVES;
+  const void* fn = reinterpret_cast<const void*>(&paged_prefill_mfma<T, DP, WAVES, 1>);
+  static const int per_cu = resident_per_cu(fn, 64 * WAVES);
+  const int64_t wgs = ((int64_t)a.T + QB - 1) / QB * a.H;
+  // Measured on MI355X: with two workgroups per CU and a grid that is
+  // resident at once, pairing long with short query tiles per CU cuts the
+  // 2048-row chunks by 8-19%. With one per CU (fp32 and the 256-wide bf16 /
+  // f16 tiles fill the LDS) the grid runs in dynamic rounds, where the
+  // longest-first order is better (the pairing cost fp32 16-33%).
+  PrefillArgs b = a;
+  b.pair_round = (per_cu == 2 && (a.H & 7) == 0 && a.cus % 8 == 0 && wgs > a.cus && wgs <= 2 * a.cus)
+                     ? a.cus / 8 : 0;
+  hipLaunchKernelGGL((paged_prefill_mfma<T, DP, WAVES, 1>), dim3((unsigned)wgs), dim3(64 * WAVES), 0,
+                     stream, b);
+  return hipGetLastError();
+}
+
 template <typename T, int DP>
 hipError_t launch_dp(const PrefillArgs& a, int waves, int qpw, hipStream_t stream) {
-  const int qb = 16 * waves * qpw;
-  const dim3 grid((unsigned)(((int64_t)a.T + qb - 1) / qb * a.H));
   (void)qpw;  // one 16-row block per wavefront (see launch_paged_prefill)
-  if (waves == 4)
-    hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 4, 1>), grid, dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((paged_prefill_mfma<T, DP, 2, 1>), grid, dim3(128), 0, stream, a);
-  return hipGetLastError();
+  return waves == 4 ? launch_waves<T, DP, 4>(a, stream) : launch_waves<T, DP, 2>(a, stream);
 }
 
 }  // namespace
