@@ -145,8 +145,8 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   // Two stages: tile t is read from one while tile t+1 is written to the other.
   __shared__ __align__(16) T k_lds[2][kTileKeys * KROW];
   __shared__ __align__(16) T vt_lds[2][DP * VROW];
-  __shared__ KeyRows slots[2][kTileKeys];
-  __shared__ uint64_t slot_valid[2];  // bit k: key k of the tile has K and V rows
+  __shared__ KeyRows slots[2][kTileKeys];  // tile t's rows in stage t & 1
+  __shared__ uint64_t slot_valid[4];      // tile t in stage t & 3; bit k: key k has K and V rows
 
   // 1-D grid of nq * H workgroups, dispatched round-robin over the XCDs
   // (workgroup id mod 8). With H a multiple of 8, every query tile of head h
@@ -208,8 +208,9 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
 
   // Staging registers: item j of this thread covers 4 keys x one chunk, for K
   // (keys vary slowest: lanes sweep the head dim) and V (lanes sweep keys).
-  uint4 kr[IPT][4], vr[IPT][4];
-  auto load_tile = [&](int sb) {
+  // Two sets: tile t is staged in set t & 1, loaded two tiles ahead.
+  uint4 kr0[IPT][4], vr0[IPT][4], kr1[IPT][4], vr1[IPT][4];
+  auto load_tile = [&](uint4 (&kr)[IPT][4], uint4 (&vr)[IPT][4], int sb) {
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
       const int it = tid + NT * j;
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
       }
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](const uint4 (&kr)[IPT][4], const uint4 (&vr)[IPT][4], int buf) {
     T* kl = k_lds[buf];
     T* vl = vt_lds[buf];
 #pragma unroll
@@ -277,7 +278,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     l_part[b] = 0.f;
   }
 
-  auto compute = [&](int buf, int kt0) {
+  auto compute = [&](int buf, int vb, int kt0) {
     const T* kl = k_lds[buf];
     const T* vl = vt_lds[buf];
     // ---- S^T blocks: lane holds keys kt0 + 16*kb + 4*g + i of query column `col`
@@ -314,7 +315,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     // (scale > 0, so the maximum of raw scores gives the maximum of scaled ones).
     // The tile's validity mask is wave-uniform: read it into scalar registers
     // so interior tiles take a branch with no masking work at all.
-    const uint64_t vm_lds = slot_valid[buf];
+    const uint64_t vm_lds = slot_valid[vb];
     const uint32_t vm_lo = __builtin_amdgcn_readfirstlane((uint32_t)vm_lds);
     const uint32_t vm_hi = __builtin_amdgcn_readfirstlane((uint32_t)(vm_lds >> 32));
     const bool full = kt0 + kTileKeys - 1 <= wave_first && (vm_lo & vm_hi) == 0xffffffffu;
@@ -412,42 +413,85 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     }
   };
 
-  // ---- pipeline: tile t+1 is in registers while tile t is computed; its
-  // block-table slots are in LDS two tiles ahead.
   // Wave 0 (tid < 64, all lanes active) publishes a tile's K/V row offsets
   // and which of its keys have them.
-  auto put_slots = [&](int sb, const KeyRows& rows) {
-    slots[sb][tid] = rows;
+  auto put_slots = [&](int tile, const KeyRows& rows) {
+    slots[tile & 1][tid] = rows;
     const uint64_t vm = __builtin_amdgcn_ballot_w64(rows.k >= 0 && rows.v >= 0);
-    if (tid == 0) slot_valid[sb] = vm;
+    if (tid == 0) slot_valid[tile & 3] = vm;
   };
   KeyRows slot_next{-1, -1};
-  if (tid < kTileKeys) {
-    put_slots(0, key_rows(a, tid, kv_end));
-    if (ntiles > 1) slot_next = key_rows(a, kTileKeys + tid, kv_end);
-  }
-  __syncthreads();
-  load_tile(0);
-  if (tid < kTileKeys) {
-    put_slots(1, slot_next);
-    if (ntiles > 2) slot_next = key_rows(a, 2 * kTileKeys + tid, kv_end);
-  }
-  store_tile(0);
-  __syncthreads();
-  if (ntiles > 1) load_tile(1);
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int kt0 = t * kTileKeys;
-    if (wave_active && kt0 <= wave_last) compute(t & 1, kt0);
-    if (t + 1 < ntiles) {
-      if (tid < kTileKeys) {
-        put_slots(t & 1, slot_next);   // tile t+2
-        if (t + 3 < ntiles) slot_next = key_rows(a, (t + 3) * kTileKeys + tid, kv_end);
-      }
-      store_tile((t + 1) & 1);
+  if constexpr (k16) {
+    // ---- pipeline (2-byte types): tile t+1 waits in registers while tile t
+    // is computed, and the loads of tile t+2 are in flight (two compute steps
+    // from load to use); block-table rows are resolved one tile before their
+    // loads. Measured on MI355X: 16% faster than one tile ahead for a 512-row
+    // chunk after a 512-token prefix, equal on 2048-row chunks.
+    if (tid < kTileKeys) {
+      put_slots(0, key_rows(a, tid, kv_end));
+      put_slots(1, key_rows(a, kTileKeys + tid, kv_end));
+      slot_next = key_rows(a, 2 * kTileKeys + tid, kv_end);
     }
     __syncthreads();
-    if (t + 2 < ntiles) load_tile(t & 1);
+    load_tile(kr0, vr0, 0);
+    if (ntiles > 1) load_tile(kr1, vr1, 1);
+    store_tile(kr0, vr0, 0);
+    __syncthreads();  // every wave has read tile 0's rows (stage 0)
+    if (tid < kTileKeys) {
+      put_slots(2, slot_next);
+      slot_next = key_rows(a, 3 * kTileKeys + tid, kv_end);
+    }
+    __syncthreads();
+    if (ntiles > 2) load_tile(kr0, vr0, 0);  // tile 2 (rows stage 2 & 1 = 0)
+
+    // One step: compute tile t, stage tile t+1 (held in set kn/vn) into LDS,
+    // publish the rows of tile t+3, then load tile t+3 into the freed set.
+    auto step = [&](int t, uint4 (&kn)[IPT][4], uint4 (&vn)[IPT][4]) {
+      const int kt0 = t * kTileKeys;
+      if (wave_active && kt0 <= wave_last) compute(t & 1, t & 3, kt0);
+      if (t + 1 < ntiles) store_tile(kn, vn, (t + 1) & 1);
+      if (tid < kTileKeys && t + 3 < ntiles) {
+        put_slots(t + 3, slot_next);
+        slot_next = key_rows(a, (t + 4) * kTileKeys + tid, kv_end);
+      }
+      __syncthreads();
+      if (t + 3 < ntiles) load_tile(kn, vn, (t + 3) & 1);
+    };
+    for (int t = 0; t < ntiles; t += 2) {
+      step(t, kr1, vr1);
+      if (t + 1 < ntiles) step(t + 1, kr0, vr0);
+    }
+  } else {
+    // ---- pipeline (fp32, whose registers allow one staging set): tile t+1 is
+    // in registers while tile t is computed; its block-table rows are in LDS
+    // two tiles ahead.
+    if (tid < kTileKeys) {
+      put_slots(0, key_rows(a, tid, kv_end));
+      if (ntiles > 1) slot_next = key_rows(a, kTileKeys + tid, kv_end);
+    }
+    __syncthreads();
+    load_tile(kr0, vr0, 0);
+    if (tid < kTileKeys) {
+      put_slots(1, slot_next);
+      if (ntiles > 2) slot_next = key_rows(a, 2 * kTileKeys + tid, kv_end);
+    }
+    store_tile(kr0, vr0, 0);
+    __syncthreads();
+    if (ntiles > 1) load_tile(kr0, vr0, 1);
+
+    for (int t = 0; t < ntiles; ++t) {
+      const int kt0 = t * kTileKeys;
+      if (wave_active && kt0 <= wave_last) compute(t & 1, t & 3, kt0);
+      if (t + 1 < ntiles) {
+        if (tid < kTileKeys) {
+          put_slots(t + 2, slot_next);
+          if (t + 3 < ntiles) slot_next = key_rows(a, (t + 3) * kTileKeys + tid, kv_end);
+        }
+        store_tile(kr0, vr0, (t + 1) & 1);
+      }
+      __syncthreads();
+      if (t + 2 < ntiles) load_tile(kr0, vr0, t & 1);
+    }
   }
 
   // ---- normalise and store: lane holds out[qi, h, 16*db + 4*g + 0..3]
