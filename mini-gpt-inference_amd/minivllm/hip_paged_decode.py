@@ -17,7 +17,8 @@ attention that reads it. There is no fallback: without the library or a GPU
 these functions raise.
 
 Beyond the Triton v0 backend: float32, bfloat16 and float16; head_dim up to
-512; any block size; split-context partitions for long contexts.
+512; any block size; a split of long and ragged contexts over many
+wavefronts (all sequences' blocks dealt out evenly) with a merge pass.
 
 paged_prefill_hip is the prefill counterpart (the reference's per-token
 loop, minivllm/attention.py:269-299, and its sdpa_v2 gather,
@@ -47,8 +48,10 @@ def paged_attention_batch_hip(q: torch.Tensor, pool: KVBlockPool, block_tables: 
                               split_tokens: int = 0) -> torch.Tensor:
     """One fused decode-attention pass over the paged pool; caller already wrote new KV.
 
-    Returns a fresh [B, H, D] tensor of q.dtype. ``split_tokens`` sets the
-    context partition size (0 = automatic).
+    Returns a fresh [B, H, D] tensor of q.dtype. ``split_tokens`` = 0 lets
+    the library split the work (evenly over a fixed number of wavefronts
+    when contexts span several partitions); > 0 cuts every context into
+    partitions of that many tokens.
     """
     lib = _native.lib()
     _check_device(q, "q")
