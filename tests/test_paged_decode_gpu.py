@@ -228,7 +228,7 @@ def test_decode_microbench_invariances():
     assert torch.equal(again.view(torch.int32), base.view(torch.int32))
 
 
-@pytest.mark.parametrize("B", [7, 200])
+@pytest.mark.parametrize("B", [7, 200, 1000])
 def test_balanced_split_with_empty_and_one_token_contexts(B):
     """The automatic split spreads every sequence's blocks evenly over the
     waves (several sequences per wave, several waves per sequence); rows with
