@@ -57,7 +57,8 @@ enum mgi_itype { MGI_I32 = 0, MGI_I64 = 1 };
 /* Thread-local description of the last failing call ("" if none). */
 const char* mgi_last_error(void);
 
-/* ABI version of this library (major*100 + minor). */
+/* ABI version of this library (major*100 + minor). 1.01 added
+ * mgi_paged_decode_balanced_waves and the even split of split_tokens = 0. */
 int mgi_abi_version(void);
 
 /*

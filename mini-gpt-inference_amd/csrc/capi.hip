@@ -137,11 +137,12 @@ WorkspaceLayout workspace_layout(int64_t B, int64_t H, int64_t D, const SplitPla
   return w;
 }
 
-// Tokens loaded per pipeline stage of the fast kernel: 16 for bf16 and 8 for
-// f32 (32 KiB of K+V per stage and wavefront at head_dim 128; two stages in
-// flight), or the largest S allows. Measured on MI355X this beats smaller
-// stages at higher occupancy. MINIVLLM_HIP_TOKENS_PER_STEP (4, 8, or 16 for
-// bf16) overrides the choice when S allows it (tuning).
+// Tokens loaded per pipeline stage of the fast kernel: 16 for bf16 and f16
+// and 8 for f32 (32 KiB of K+V per stage and wavefront at head_dim 128; two
+// stages in flight), or the largest S allows. Measured on MI355X this beats
+// smaller stages at higher occupancy. MINIVLLM_HIP_TOKENS_PER_STEP (8 or 16
+// for the 2-byte types, 4 or 8 for f32) overrides the choice when S allows it
+// (tuning).
 int tokens_per_step_override() {
   static const int v = [] {
     const char* e = std::getenv("MINIVLLM_HIP_TOKENS_PER_STEP");
@@ -162,7 +163,7 @@ extern "C" {
 
 const char* mgi_last_error(void) { return g_err.c_str(); }
 
-int mgi_abi_version(void) { return 100; }
+int mgi_abi_version(void) { return 101; }
 
 int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                       int64_t split_tokens) {

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.lib()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mgi_abi_version() == 100
+    assert lib.mgi_abi_version() == 101
 
 
 def test_split_tokens_and_workspace_sizes():
