@@ -136,15 +136,20 @@ def test_generic_path_shapes(dtype, D, S):
     np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)), **tol)
 
 
+@pytest.mark.parametrize("split", [0, 64], ids=["auto", "partitions"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_int32_indices_and_strided_q(dtype):
+def test_int32_indices_and_strided_q(dtype, split):
     ctx = [5, 77, 190]
     q, pool, tables, lens, layer = _small_case(3, 8, 128, 16, ctx, dtype, seed=11)
     wide = torch.randn(3, 8, 256).to(dtype)
     wide[..., ::2] = q
     q_strided = wide[..., ::2]
     assert q_strided.stride(-1) == 2
-    got = hip(q_strided, fx.pool_to_device(pool, DEV), tables.int(), lens.int(), layer, split_tokens=64)
+    # a table wider than one partition, so the automatic split divides the work
+    wide_tables = torch.nn.functional.pad(tables, (0, 40 - tables.shape[1]), value=-1)
+    assert (split == 0) == (hpd._native.lib().mgi_paged_decode_balanced_waves(3, 8, 128, 16, 40, split) > 0)
+    got = hip(q_strided, fx.pool_to_device(pool, DEV), wide_tables.int(), lens.int(), layer,
+              split_tokens=split)
     np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)),
                                **tol_for(dtype))
 
