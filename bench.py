@@ -59,6 +59,10 @@ def parse_args():
     ap.add_argument("--e2e-requests", type=int, default=256)
     ap.add_argument("--prefill", action="store_true",
                     help="also time the paged prefill kernel (implied unless --no-extras)")
+    ap.add_argument("--e2e-trace", action="store_true",
+                    help="run only the full runtime once (HIP prefill and decode, eager) and print "
+                         "its statistics with the decode attention's algorithmic KV bytes, for a "
+                         "kernel trace")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run a device-to-device copy of this many MiB (3 times) so rocprof "
                          "counters can be scaled by a kernel of known traffic")
@@ -147,6 +151,37 @@ def e2e_model(dev):
         model.set_decode_attention_backend("hip")
         _E2E_MODEL["m"] = model
     return _E2E_MODEL["m"]
+
+
+def e2e_trace_line(n_requests: int, dev):
+    """One run of the full runtime (HIP prefill and decode, eager) that also
+    sums the decode attention's algorithmic KV bytes: every decode row reads
+    its context, H*D*2*2 bytes per token and layer. The accounting adds host
+    work, so this run is for kernel traces, not for tokens/s."""
+    import torch
+
+    import _e2e
+
+    spec = _e2e.RuntimeSpec(n_requests=n_requests, prefill_mode="hip")
+    model = e2e_model(dev)
+    model.set_prefill_fastpath_mode("hip")
+    rt, seqs = _e2e.make_runtime(spec, model, _e2e.make_prompts(spec), dev, torch.bfloat16)
+    acc = {"sum_ctx": 0, "calls": 0}
+    inner = rt.runner.decode_batch
+
+    def decode_batch(sequences):
+        acc["sum_ctx"] += sum(s.length + 1 for s in sequences)
+        acc["calls"] += 1
+        return inner(sequences)
+
+    rt.runner.decode_batch = decode_batch
+    stats = _e2e.run_to_completion(rt, seqs)
+    torch.cuda.synchronize()
+    head_dim = spec.n_embd // spec.n_head
+    stats.update({"decode_steps": acc["calls"], "decode_sum_ctx": acc["sum_ctx"],
+                  "decode_attention_calls": acc["calls"] * spec.n_layer,
+                  "decode_attention_kv_bytes": acc["sum_ctx"] * spec.n_head * head_dim * 2 * 2 * spec.n_layer})
+    return stats
 
 
 def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2",
@@ -492,6 +527,10 @@ def main() -> None:
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.e2e_trace:
+        with torch.inference_mode():
+            print(json.dumps(e2e_trace_line(args.e2e_requests, dev)), flush=True)
+        return
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float32
     B, H, D, S, N = 64, 32, 128, 16, 20000
 
