@@ -85,10 +85,13 @@ int64_t split_tokens_for(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
 // one per SIMD) and finish together, each taking at least kBalMinTokens
 // tokens. Measured on MI355X (B=64 ragged, B=256, B=8 long contexts; bf16 and
 // f32): 2-3 waves per CU are best and within noise of each other; 4 per CU is
-// 1-2% slower, and 5-6 per CU (a partial second round) up to 10% slower.
-// MINIVLLM_HIP_DECODE_BALANCED=0 turns the mode off and MINIVLLM_HIP_BAL_WAVES
-// sets the total wave count (tuning).
-constexpr int64_t kBalMinTokens = 256;
+// 1-2% slower, and 5-6 per CU (a partial second round) up to 10% slower. A
+// floor of 64 tokens per wave halves small calls against 256 (B=8 x 256
+// tokens, 16 heads: 16.9 against 34.6 us) and leaves large ones unchanged;
+// 16 and 32 are no better. MINIVLLM_HIP_DECODE_BALANCED=0 turns the mode off,
+// MINIVLLM_HIP_BAL_WAVES sets the total wave count and
+// MINIVLLM_HIP_BAL_MIN_TOKENS the floor (tuning).
+constexpr int64_t kBalMinTokens = 64;
 
 int env_int(const char* name, int dflt) {
   const char* e = std::getenv(name);
@@ -97,14 +100,16 @@ int env_int(const char* name, int dflt) {
 
 struct SplitPlan {
   int64_t P;             // partition mode: tokens per partition
-  int64_t max_parts;     // partials per (sequence, head)
+  int64_t max_parts;     // partition mode: partials per (sequence, head)
   int bal_waves;         // > 0: balanced mode, waves per head group
   int bal_min_blocks;    // balanced mode: least blocks per wave
+  int64_t n_partials;    // partial slots in the workspace
 };
 
 SplitPlan split_plan(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M, int64_t requested) {
   static const int balanced = env_int("MINIVLLM_HIP_DECODE_BALANCED", 1);
   static const int waves = env_int("MINIVLLM_HIP_BAL_WAVES", 0);
+  static const int64_t min_tokens = std::max(1, env_int("MINIVLLM_HIP_BAL_MIN_TOKENS", (int)kBalMinTokens));
   SplitPlan sp{};
   sp.P = split_tokens_for(B, H, D, S, M, requested);
   sp.max_parts = (M * S + sp.P - 1) / sp.P;
@@ -114,8 +119,10 @@ SplitPlan split_plan(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M, int6
     const int64_t groups = (H + 64 / lph - 1) / (64 / lph);
     const int64_t target = waves > 0 ? waves : 3 * (int64_t)device_cus();
     sp.bal_waves = (int)std::max<int64_t>(1, target / groups);
-    sp.bal_min_blocks = (int)((kBalMinTokens + S - 1) / S);
-    sp.max_parts = (M + sp.bal_min_blocks - 1) / sp.bal_min_blocks + 1;
+    sp.bal_min_blocks = (int)((min_tokens + S - 1) / S);
+    sp.n_partials = H * (int64_t)sp.bal_waves * 2;  // two slots per (head, wave)
+  } else if (sp.max_parts > 1) {
+    sp.n_partials = B * H * sp.max_parts;
   }
   return sp;
 }
@@ -124,12 +131,13 @@ struct WorkspaceLayout {
   size_t acc_bytes, ml_offset, cinc_offset, total;
 };
 
-// [acc: B*H*max_parts*D f32 | ml: B*H*max_parts float2 | cinc: B int32
-// (balanced mode)], each part 256-byte aligned.
-WorkspaceLayout workspace_layout(int64_t B, int64_t H, int64_t D, const SplitPlan& sp) {
+// [acc: n_partials*D f32 | ml: n_partials float2 | cinc: B int32 (balanced
+// mode)], each part 256-byte aligned. Partition mode holds B*H*max_parts
+// partials; balanced mode 2 per (head, wave), whatever B and M.
+WorkspaceLayout workspace_layout(int64_t B, int64_t D, const SplitPlan& sp) {
   WorkspaceLayout w{};
-  if (sp.max_parts <= 1) return w;
-  const int64_t n = B * H * sp.max_parts;
+  if (sp.n_partials == 0) return w;
+  const int64_t n = sp.n_partials;
   w.acc_bytes = (size_t)(n * D * 4);
   w.ml_offset = (size_t)round_up((int64_t)w.acc_bytes, kWorkspaceAlign);
   w.cinc_offset = (size_t)round_up((int64_t)w.ml_offset + n * 8, kWorkspaceAlign);
@@ -180,7 +188,7 @@ int64_t mgi_paged_decode_balanced_waves(int64_t B, int64_t H, int64_t D, int64_t
 size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                         int64_t split_tokens) {
   if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || M <= 0) return 0;
-  return workspace_layout(B, H, D, split_plan(B, H, D, S, M, split_tokens)).total;
+  return workspace_layout(B, D, split_plan(B, H, D, S, M, split_tokens)).total;
 }
 
 int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
@@ -219,7 +227,7 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   const char* vbase = static_cast<const char*>(v_pool) + layer_idx * v_pool_strides[0] * eb;
 
   const SplitPlan sp = split_plan(B, H, D, S, M, split_tokens);
-  const WorkspaceLayout ws = workspace_layout(B, H, D, sp);
+  const WorkspaceLayout ws = workspace_layout(B, D, sp);
 
   // Path selection: the fast kernel needs unit d-stride, 16-byte aligned head
   // rows, head_dim a multiple of 8 up to 256 and S a multiple of its step.
@@ -287,7 +295,7 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   a.scale_log2 = scale * 1.4426950408889634f;
   a.part_tokens = (int)sp.P;
   a.max_parts = plan.path == DecodePath::kFast ? (int)sp.max_parts : 1;
-  if (a.max_parts > 1) {
+  if (plan.path == DecodePath::kFast && sp.n_partials > 0) {
     if (!workspace) return fail(MGI_EWORKSPACE, "workspace required for split-context pass");
     if (workspace_bytes < ws.total)
       return fail(MGI_EWORKSPACE, "workspace smaller than mgi_paged_decode_workspace_bytes()");

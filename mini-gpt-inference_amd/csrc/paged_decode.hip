@@ -301,17 +301,16 @@ __device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane,
 }
 
 // Writes a wave's state: the normalised output when the sequence has one
-// piece of work, else partial j of (b, h).
+// piece of work, else the partial in workspace slot pidx.
 template <typename T>
 __device__ __forceinline__ void finish_piece(const DecodeArgs& a, int b, int h, int sub, bool lane_ok,
                                              float m, float l, const float (&acc)[8], int npieces,
-                                             int j) {
+                                             size_t pidx) {
   if (!lane_ok) return;
   if (npieces <= 1) {
     store_out<T>(a, b, h, sub, acc, l > 0.f ? 1.f / l : 0.f);
     return;
   }
-  const size_t pidx = ((size_t)b * a.H + h) * a.max_parts + j;
   float* wa = a.ws_acc + pidx * a.D;
   float4* w0 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, a.D, 0));
   float4* w1 = reinterpret_cast<float4*>(wa + Layout<T>::elem(sub, a.D, 4));
@@ -348,7 +347,7 @@ paged_decode_fast(const DecodeArgs a) {
   const int bpp = P / a.S;  // P is a multiple of S
   fold_chunk<T, LPH, TOK, FULL>(a, b, lane, lane_ok, q, koff, voff, part * bpp, (part + 1) * bpp, ctx,
                                  m, l, acc);
-  finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, nparts, part);
+  finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, nparts, ((size_t)b * a.H + h) * a.max_parts + part);
 }
 
 // Balanced mode. The blocks of all sequences, in sequence order, form one
@@ -357,9 +356,19 @@ paged_decode_fast(const DecodeArgs a) {
 // ceil(total / bal_waves)), so every wave streams the same number of blocks
 // whatever the spread of context lengths, and no wave is left running alone
 // at the end of the grid. A sequence split over several waves gets one
-// partial per wave (index w - floor(cb / Wb), cb its first block in the list),
-// combined by paged_decode_merge; a sequence inside one wave is written
-// directly.
+// partial per wave, combined by paged_decode_merge; a sequence inside one
+// wave is written directly.
+//
+// Partial slots belong to waves, not sequences: a wave writes at most two
+// partials, for the sequence it starts in (slot 0: the sequence began at or
+// before the wave's first block) and for the one it ends in (slot 1: that
+// sequence began inside the wave and runs past its end), since every other
+// sequence it touches lies wholly inside it. Slot (h, w, s) is
+// (h * bal_waves + w) * 2 + s, so the workspace holds H * bal_waves * 2
+// partials whatever B and the table width.
+__device__ __forceinline__ size_t bal_slot(const DecodeArgs& a, int h, int w, int wb, int cb) {
+  return ((size_t)h * a.bal_waves + w) * 2 + ((int64_t)w * wb >= cb ? 0 : 1);
+}
 
 __device__ __forceinline__ int bal_blocks_per_wave(int total, int waves, int min_blocks) {
   const int wb = (total + waves - 1) / waves;
@@ -458,8 +467,8 @@ paged_decode_fast_bal(const DecodeArgs a) {
                                   acc);
     pos = ch_end;
     if (pos == ce || pos == end) {
-      const int w_first = cb / wb;
-      finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, (ce - 1) / wb - w_first + 1, w - w_first);
+      finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, (ce - 1) / wb - cb / wb + 1,
+                      bal_slot(a, h, w, wb, cb));
       // Next sequence with blocks past pos (cinc[B-1] = total bounds b while pos < end).
       while (pos < end && uread(cinc, b) <= pos) ++b;
     }
@@ -490,36 +499,42 @@ paged_decode_merge(const DecodeArgs a) {
   const int D = a.D;
   const bool head_ok = h < a.H;
   const bool lane_ok = head_ok && sub * 8 < D;
+  const int hh = head_ok ? h : 0;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  int nparts;
+  int nparts, cb = 0, wb = 1, w_first = 0;
   if (a.bal_waves > 0) {
     const int total = a.ws_cinc[a.B - 1];
-    const int cb = b > 0 ? a.ws_cinc[b - 1] : 0;
+    cb = b > 0 ? a.ws_cinc[b - 1] : 0;
     const int ce = a.ws_cinc[b];
     if (ce <= cb) {  // no blocks: zeros, as for an empty context
       if (lane_ok) store_out<T>(a, b, h, sub, acc, 0.f);
       return;
     }
-    const int wb = bal_blocks_per_wave(total, a.bal_waves, a.bal_min_blocks);
-    nparts = (ce - 1) / wb - cb / wb + 1;
+    wb = bal_blocks_per_wave(total, a.bal_waves, a.bal_min_blocks);
+    w_first = cb / wb;
+    nparts = (ce - 1) / wb - w_first + 1;
   } else {
     const int ctx = clamp_ctx<T>(a, b);
     nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
   }
   if (nparts <= 1) return;  // uniform over the wave
-  const size_t base = ((size_t)b * a.H + (head_ok ? h : 0)) * a.max_parts;
+  // Workspace slot of partial j of (b, hh).
+  auto slot = [&](int j) -> size_t {
+    return a.bal_waves > 0 ? bal_slot(a, hh, w_first + j, wb, cb)
+                           : ((size_t)b * a.H + hh) * a.max_parts + j;
+  };
 
   float M = -INFINITY, L = 0.f;
   for (int p0 = 0; p0 < nparts; p0 += CH) {
     float2 ml = make_float2(-INFINITY, 0.f);
-    if (head_ok && sub < CH && p0 + sub < nparts) ml = a.ws_ml[base + p0 + sub];
+    if (head_ok && sub < CH && p0 + sub < nparts) ml = a.ws_ml[slot(p0 + sub)];
     float4 x0[CH], x1[CH];
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       if (lane_ok && p0 + j < nparts) {
-        const float* wa = a.ws_acc + (base + p0 + j) * D;
+        const float* wa = a.ws_acc + slot(p0 + j) * D;
         x0[j] = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 0));
         x1[j] = *reinterpret_cast<const float4*>(wa + Layout<T>::elem(sub, D, 4));
       } else {
@@ -638,7 +653,7 @@ static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_
                           : reinterpret_cast<const void*>(&paged_decode_fast<T, LPH, TOK, false>);
     e = launch(fn, dim3(ngroups, (unsigned)a.max_parts, (unsigned)a.B), dim3(64), a, stream);
   }
-  if (e != hipSuccess || a.max_parts <= 1) return e;
+  if (e != hipSuccess || (a.bal_waves <= 0 && a.max_parts <= 1)) return e;
   return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH>), dim3(ngroups, (unsigned)a.B),
                 dim3(64), a, stream);
 }
