@@ -4,6 +4,7 @@
 // paged_attention_batch_triton_v0 (minivllm/triton_paged_decode.py:109-144);
 // nothing here reads device memory or synchronises the stream.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <string>
@@ -44,15 +45,16 @@ constexpr int64_t kMaxBlocksPerPart = 128;
 // Compute units of the current device (256 on MI355X; 256 when no device is
 // visible, e.g. for host-only size queries).
 int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];  // 0 = not queried yet (zero-initialised)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    cached[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-                   n > 0) ? n : 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (!n) {
+    int q = 0;
+    n = (hipDeviceGetAttribute(&q, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && q > 0) ? q : 256;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // Partition size in tokens: a multiple of S, at most kMaxBlocksPerPart blocks
