@@ -625,10 +625,14 @@ def main() -> None:
             extras["decode_step_latency_eager_vs_graph"] = decode_step_latency(dev)
             extras["decode_metadata_prep"] = metadata_prep_line(dev)
             hip = extras["e2e_runtime_bf16_preemption_hip_prefill"]
+            hip_g = extras["e2e_runtime_bf16_preemption_hip_prefill_graphs"]
             e2e_summary = {"decode_tokens_per_s": hip["decode_tok_s_in_decode_phase"],
                            "output_tokens_per_s": hip["output_tok_s"],
+                           "decode_tokens_per_s_with_graphs": hip_g["decode_tok_s_in_decode_phase"],
+                           "output_tokens_per_s_with_graphs": hip_g["output_tok_s"],
                            "workload": "full runtime, 256 requests, MiniGPT dim 2048 x 12 layers, bf16, "
-                                       "HIP decode + HIP prefill, recompute preemption"}
+                                       "HIP decode + HIP prefill, recompute preemption (eager; "
+                                       "'with_graphs': decode steps of <= 64 rows replay HIP graphs)"}
             _E2E_MODEL.clear()
             torch.cuda.empty_cache()
 
