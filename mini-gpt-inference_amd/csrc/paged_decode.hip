@@ -218,17 +218,20 @@ __device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane,
       phys_hi = (e >= 0 && e < a.N) ? (int)e : -1;
     }
 
-    // Issues the K/V loads of step s (clamped to the last step: a step past
-    // the chunk re-reads that step's lines, which are cache-resident, so every
-    // iteration issues the same number of loads). Returns the number of valid
-    // tokens of step s (0 past the chunk or for a masked block).
+    // Issues the K/V loads of step s and returns its number of valid tokens
+    // (0 past the chunk or for a masked block). Every iteration issues the
+    // same loads, with no branch around them; a step past the chunk points
+    // every lane at the same 16 bytes of the last step's first row (one line
+    // per wave: the streaming loads are non-temporal, so re-reading the whole
+    // last step would fetch it from HBM again).
     auto issue = [&](int s, Step<T, TOK>& st) -> int {
-      const int sc = s < nsteps ? s : nsteps - 1;
+      const bool past = s >= nsteps;
+      const int sc = past ? nsteps - 1 : s;
       const int rel = sc / steps_per_blk;
       const int off = (sc - rel * steps_per_blk) * TOK;
       const int phys = rel < 64 ? __builtin_amdgcn_readlane(phys_lo, rel)
                                 : __builtin_amdgcn_readlane(phys_hi, rel - 64);
-      const int nvalid = min(TOK, t_end - (t_begin + sc * TOK));
+      const int nvalid = past ? 1 : min(TOK, t_end - (t_begin + sc * TOK));
       const int64_t pb = phys >= 0 ? phys : 0;  // a masked block is read from block 0, never used
       const auto krs = make_rsrc(kl + (pb * a.k_sn + (int64_t)off * a.k_ss) * EB);
       const auto vrs = make_rsrc(vl + (pb * a.v_sn + (int64_t)off * a.v_ss) * EB);
@@ -239,7 +242,7 @@ __device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane,
         const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * k_row);
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-          if (FULL || lane_ok) st.k[t][j] = buffer_load16(krs, koff[j], so);
+          if (FULL || lane_ok) st.k[t][j] = buffer_load16(krs, past ? 0u : koff[j], so);
           else st.k[t][j] = make_uint4(0u, 0u, 0u, 0u);
         }
       }
@@ -248,11 +251,11 @@ __device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane,
         const uint32_t so = (uint32_t)((t < nvalid ? t : nvalid - 1) * v_row);
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-          if (FULL || lane_ok) st.v[t][j] = buffer_load16(vrs, voff[j], so);
+          if (FULL || lane_ok) st.v[t][j] = buffer_load16(vrs, past ? 0u : voff[j], so);
           else st.v[t][j] = make_uint4(0u, 0u, 0u, 0u);
         }
       }
-      return (s < nsteps && phys >= 0) ? nvalid : 0;
+      return (!past && phys >= 0) ? nvalid : 0;
     };
 
     // Folds one step into the online softmax.
