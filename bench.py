@@ -632,7 +632,7 @@ def main() -> None:
                            "output_tokens_per_s_with_graphs": hip_g["output_tok_s"],
                            "workload": "full runtime, 256 requests, MiniGPT dim 2048 x 12 layers, bf16, "
                                        "HIP decode + HIP prefill, recompute preemption (eager; "
-                                       "'with_graphs': decode steps of <= 64 rows replay HIP graphs)"}
+                                       "'with_graphs': decode steps of <= 128 rows replay HIP graphs)"}
             _E2E_MODEL.clear()
             torch.cuda.empty_cache()
 

@@ -30,11 +30,13 @@ from .kv_block_pool import KVBlockPool
 
 # Batch buckets captured by default. On MI355X a replayed step of the
 # dim-2048, 12-layer model at context 512 takes 1.3 ms against 2.1-2.2 ms of
-# eager launches up to 16 rows and 1.86 against 2.16 ms at 64 rows. At 256
-# rows the step is bound by the GPU (4.27 vs 4.24 ms), and in the full
-# preemption runtime padding 129-256-row batches to 256 made the decode phase
-# 25% slower than eager, so larger batches run eagerly.
-DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64)
+# eager launches up to 16 rows and 1.86 against 2.16 ms at 64 rows; at 256
+# rows the step is bound by the GPU (4.27 vs 4.24 ms). In the full preemption
+# runtime (decode tokens/s): eager 40.0-41.1 k, buckets up to 64 rows 42.9 k,
+# up to 128 rows 43.6-43.8 k, up to 256 rows 42.4-42.5 k (padding 129-256
+# rows to 256 doubles the GEMM and elementwise work of those steps; padding
+# rows cost the attention nothing), so 129+ row batches run eagerly.
+DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128)
 
 
 def pack_decode_metadata(tokens, positions, slots, tables, B_pad: int, M: int) -> torch.Tensor:
