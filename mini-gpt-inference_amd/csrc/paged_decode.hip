@@ -7,18 +7,22 @@
 // through block_tables[b, 0 : ceil(ctx_b / S)]. Table entries past the
 // context and pool slots past the context are never dereferenced.
 //
-// Fast path (paged_decode_fast): one wavefront owns HPW = 64/LPH heads of one
-// sequence and one context partition. LPH lanes share a head row, each lane
-// owning 8 elements of head_dim, so one 16-byte load instruction of the wave
-// reads a contiguous run of HPW head rows of one token (1 KiB for bf16,
-// D=128). Per step the wave issues TOK tokens of K and V loads up front
-// (32 KiB in flight per wave for bf16, TOK=16), then forms the TOK scores with
-// packed bf16 dot products and a DPP all-reduce inside each 16-lane row, and
-// folds the step into an fp32 online softmax kept in the log2 domain.
-// Decode attention is HBM-bound (~1 flop/byte), so there is no MFMA and no
-// LDS staging: every lane loads exactly the bytes it consumes.
+// Fast path (fold_chunk, run by paged_decode_fast_bal or paged_decode_fast):
+// a wavefront owns HPW = 64/LPH heads and streams a run of blocks of one
+// sequence. LPH lanes share a head row, each lane owning 8 elements of
+// head_dim, so one 16-byte load instruction of the wave reads a contiguous
+// run of HPW head rows of one token (1 KiB for bf16, D=128). Per step the
+// wave issues TOK tokens of K and V loads up front (32 KiB in flight per wave
+// for bf16, TOK=16; non-temporal, as every byte is read once), then forms the
+// TOK scores with packed 16-bit dot products and a DPP all-reduce inside each
+// row of LPH lanes, and folds the step into an fp32 online softmax kept in
+// the log2 domain. Decode attention is HBM-bound (~1 flop/byte), so there is
+// no MFMA and no LDS staging: every lane loads exactly the bytes it consumes.
 //
-// Contexts longer than one partition write (max, sum, unnormalised output)
+// Work split: paged_decode_fast_bal deals the blocks of all sequences out
+// evenly to a fixed number of wavefronts (the automatic choice);
+// paged_decode_fast cuts each context into partitions of part_tokens tokens.
+// A sequence whose work is split writes (max, sum, unnormalised output)
 // partials that paged_decode_merge combines:
 //   M = max_p m_p,  L = sum_p l_p 2^(m_p - M),  O = sum_p O_p 2^(m_p - M) / L.
 //
