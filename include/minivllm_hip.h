@@ -112,14 +112,20 @@ int mgi_kv_append(void* k_pool, void* v_pool,
  *
  * split_tokens: 0 lets the library split the work. When a table is wider
  * than one partition and B <= 4096 it splits evenly: the blocks of all
- * sequences, in sequence order, are dealt out in equal runs to a fixed
- * number of wavefronts (mgi_paged_decode_balanced_waves), whatever the spread
- * of context lengths. Otherwise, and for split_tokens > 0 (rounded to a
- * multiple of S), each context is cut into partitions of split_tokens
- * tokens. Either way, a sequence whose work is split writes (max, sum,
- * unnormalised output) partials that a second pass merges.
+ * sequences, in sequence order, are cut into equal segments, one per
+ * wavefront of a fixed count (mgi_paged_decode_balanced_waves), whatever the
+ * spread of context lengths; each wavefront streams most of its segment and
+ * the rest of every segment goes, in small runs, to whichever wavefronts
+ * finish first. Otherwise, and for split_tokens > 0 (rounded to a multiple
+ * of S), each context is cut into partitions of split_tokens tokens. Either
+ * way, a sequence whose work is split writes (max, sum, unnormalised output)
+ * partials that a second pass merges. The output does not depend on which
+ * wavefront streams which run: calls with the same inputs give the same
+ * bits.
  * workspace must hold mgi_paged_decode_workspace_bytes(...) bytes for the
- * same (B, H, D, S, M, split_tokens); it may be NULL when that is 0.
+ * same (B, H, D, S, M, split_tokens); it may be NULL when that is 0. Its
+ * contents need no initialisation and are not meaningful after the call.
+ * Calls that overlap in time (other streams) need separate workspaces.
  */
 int mgi_paged_decode(void* out, const int64_t* out_strides, /* [3] */
                      const void* q, const int64_t* q_strides, /* [3] */

@@ -100,11 +100,26 @@ int env_int(const char* name, int dflt) {
   return e ? std::atoi(e) : dflt;
 }
 
+// Balanced mode's ticket claims (see paged_decode_fast_bal): each wave's own
+// claim covers kBalTier1Sixteenths/16 of its segment and the rest is cut into
+// up to kBalTier2PerWave claims taken by ticket. Measured on MI355X against
+// no ticket claims (16/16): +1.5% at bf16 B=64 x 512-4096, +3% in f32, +1.6%
+// at B=256 x 128-2048, +2.3% at B=8 x 32k-128k, +1.2% at a fixed 1024
+// context, equal at 512; (14, 3) was best or tied among 12-15 sixteenths and
+// 3-6 claims. MINIVLLM_HIP_BAL_TIER1 (sixteenths, 1-16) and
+// MINIVLLM_HIP_BAL_TIER2 (claims per segment, 0 turns them off) override
+// the choice (tuning; read on every call).
+constexpr int kBalTier1Sixteenths = 14;
+constexpr int kBalTier2PerWave = 3;
+
 struct SplitPlan {
   int64_t P;             // partition mode: tokens per partition
   int64_t max_parts;     // partition mode: partials per (sequence, head)
   int bal_waves;         // > 0: balanced mode, waves per head group
-  int bal_min_blocks;    // balanced mode: least blocks per wave
+  int bal_min_blocks;    // balanced mode: least blocks per claim
+  int bal_tier1_16ths;   // balanced mode: share of the list in the waves' own claims
+  int bal_tier2;         // balanced mode: ticket claims per wave's segment (at most)
+  int64_t bal_groups;    // balanced mode: head groups (one ticket counter each)
   int64_t n_partials;    // partial slots in the workspace
 };
 
@@ -122,7 +137,11 @@ SplitPlan split_plan(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M, int6
     const int64_t target = waves > 0 ? waves : 3 * (int64_t)device_cus();
     sp.bal_waves = (int)std::max<int64_t>(1, target / groups);
     sp.bal_min_blocks = (int)((min_tokens + S - 1) / S);
-    sp.n_partials = H * (int64_t)sp.bal_waves * 2;  // two slots per (head, wave)
+    sp.bal_tier1_16ths = std::min(16, std::max(1, env_int("MINIVLLM_HIP_BAL_TIER1", kBalTier1Sixteenths)));
+    sp.bal_tier2 = std::min(64, std::max(0, env_int("MINIVLLM_HIP_BAL_TIER2", kBalTier2PerWave)));
+    sp.bal_groups = groups;
+    // two slots per (head, claim); 1 + bal_tier2 claims per wave's segment
+    sp.n_partials = H * (int64_t)sp.bal_waves * (1 + sp.bal_tier2) * 2;
   } else if (sp.max_parts > 1) {
     sp.n_partials = B * H * sp.max_parts;
   }
@@ -130,12 +149,14 @@ SplitPlan split_plan(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M, int6
 }
 
 struct WorkspaceLayout {
-  size_t acc_bytes, ml_offset, cinc_offset, total;
+  size_t acc_bytes, ml_offset, cinc_offset, ticket_offset, total;
 };
 
-// [acc: n_partials*D f32 | ml: n_partials float2 | cinc: B int32 (balanced
-// mode)], each part 256-byte aligned. Partition mode holds B*H*max_parts
-// partials; balanced mode 2 per (head, wave), whatever B and M.
+// [acc: n_partials*D f32 | ml: n_partials float2 | cinc: B int32 | ticket:
+// one int32 per head group (the last two in balanced mode only)], acc, ml
+// and cinc 256-byte aligned. Partition mode holds B*H*max_parts partials;
+// balanced mode 2 per (head, claim), whatever B and M. Nothing in it needs
+// initialising.
 WorkspaceLayout workspace_layout(int64_t B, int64_t D, const SplitPlan& sp) {
   WorkspaceLayout w{};
   if (sp.n_partials == 0) return w;
@@ -143,7 +164,9 @@ WorkspaceLayout workspace_layout(int64_t B, int64_t D, const SplitPlan& sp) {
   w.acc_bytes = (size_t)(n * D * 4);
   w.ml_offset = (size_t)round_up((int64_t)w.acc_bytes, kWorkspaceAlign);
   w.cinc_offset = (size_t)round_up((int64_t)w.ml_offset + n * 8, kWorkspaceAlign);
-  w.total = sp.bal_waves > 0 ? w.cinc_offset + (size_t)(B * 4) : w.ml_offset + (size_t)(n * 8);
+  w.ticket_offset = w.cinc_offset + (size_t)(B * 4);
+  w.total = sp.bal_waves > 0 ? w.ticket_offset + (size_t)(sp.bal_groups * 4)
+                             : w.ml_offset + (size_t)(n * 8);
   return w;
 }
 
@@ -307,7 +330,11 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
     if (sp.bal_waves > 0) {
       a.bal_waves = sp.bal_waves;
       a.bal_min_blocks = sp.bal_min_blocks;
+      a.bal_tier1_16ths = sp.bal_tier1_16ths;
+      a.bal_tier2 = sp.bal_tier2;
+      a.bal_claims = sp.bal_waves * (1 + sp.bal_tier2);
       a.ws_cinc = reinterpret_cast<int*>(static_cast<char*>(workspace) + ws.cinc_offset);
+      a.ws_ticket = reinterpret_cast<int*>(static_cast<char*>(workspace) + ws.ticket_offset);
     }
   }
 

@@ -31,10 +31,14 @@ struct DecodeArgs {
   int part_tokens;    // partition mode: tokens per context partition (multiple of S)
   int max_parts;      // partials per (sequence, head) the workspace holds
   int bal_waves;      // > 0: balanced mode with this many waves per head group
-  int bal_min_blocks; // balanced mode: least blocks per wave
+  int bal_min_blocks; // balanced mode: least blocks per claim
+  int bal_tier1_16ths;// balanced mode: share of each segment in its wave's own claim (16ths)
+  int bal_tier2;      // balanced mode: ticket claims per segment, at most (0: none)
+  int bal_claims;     // balanced mode: bal_waves * (1 + bal_tier2), partial slot pairs per head
   float* ws_acc;      // [B, H, max_parts, D] unnormalised partial outputs
   float2* ws_ml;      // [B, H, max_parts]    partial (max, sum), log2 domain
   int* ws_cinc;       // balanced mode: [B] inclusive prefix sums of blocks per sequence
+  int* ws_ticket;     // balanced mode: one ticket counter per head group
 };
 
 // KV append / scatter. Pool pointers already point at layer layer_idx.

@@ -19,9 +19,11 @@
 // the log2 domain. Decode attention is HBM-bound (~1 flop/byte), so there is
 // no MFMA and no LDS staging: every lane loads exactly the bytes it consumes.
 //
-// Work split: paged_decode_fast_bal deals the blocks of all sequences out
-// evenly to a fixed number of wavefronts (the automatic choice);
-// paged_decode_fast cuts each context into partitions of part_tokens tokens.
+// Work split: paged_decode_fast_bal deals the blocks of all sequences out to
+// a fixed number of wavefronts, most of them as each wave's own claim and the
+// rest as small claims that waves draw by ticket once their own is done, so
+// faster XCDs take more (the automatic choice); paged_decode_fast cuts each
+// context into partitions of part_tokens tokens.
 // A sequence whose work is split writes (max, sum, unnormalised output)
 // partials that paged_decode_merge combines:
 //   M = max_p m_p,  L = sum_p l_p 2^(m_p - M),  O = sum_p O_p 2^(m_p - M) / L.
@@ -358,28 +360,87 @@ paged_decode_fast(const DecodeArgs a) {
 }
 
 // Balanced mode. The blocks of all sequences, in sequence order, form one
-// list of total = sum_b ceil(ctx_b / S) blocks. Wave w of each head group
-// takes the blocks [w*Wb, (w+1)*Wb) of that list, Wb = max(bal_min_blocks,
-// ceil(total / bal_waves)), so every wave streams the same number of blocks
-// whatever the spread of context lengths, and no wave is left running alone
-// at the end of the grid. A sequence split over several waves gets one
-// partial per wave, combined by paged_decode_merge; a sequence inside one
-// wave is written directly.
+// list of total = sum_b ceil(ctx_b / S) blocks, cut into P equal segments
+// (P = bal_waves, the waves of one head group) of Lw = max(bal_min_blocks,
+// ceil(total / P)) blocks, and each segment into claims: contiguous runs of
+// the list that one wave streams. A sequence split over several claims gets
+// one partial per claim, combined by paged_decode_merge; a sequence inside
+// one claim is written directly.
 //
-// Partial slots belong to waves, not sequences: a wave writes at most two
-// partials, for the sequence it starts in (slot 0: the sequence began at or
-// before the wave's first block) and for the one it ends in (slot 1: that
-// sequence began inside the wave and runs past its end), since every other
-// sequence it touches lies wholly inside it. Slot (h, w, s) is
-// (h * bal_waves + w) * 2 + s, so the workspace holds H * bal_waves * 2
-// partials whatever B and the table width.
-__device__ __forceinline__ size_t bal_slot(const DecodeArgs& a, int h, int w, int wb, int cb) {
-  return ((size_t)h * a.bal_waves + w) * 2 + ((int64_t)w * wb >= cb ? 0 : 1);
-}
+// Segment w holds wave w's own claim (about bal_tier1_16ths/16 of it) and R
+// ticket claims of a blocks each (R <= bal_tier2, fewer when a would drop
+// below bal_min_blocks). A wave streams its own claim, then draws tickets
+// from its head group's counter until they run out; ticket t is claim
+// 1 + t / P of segment t % P, so the tickets sweep the whole list. The waves
+// of a head group are spread over all XCDs (see paged_decode_fast_bal), and
+// faster XCDs draw more tickets, so the grid ends together. Measured on
+// MI355X, the XCDs of one chip stream at different rates (the slowest about
+// 15% behind the fastest at the same load): an equal split leaves the fast
+// XCDs idle for the last tenth of the kernel.
+//
+// The ticket counter is zeroed by wave 0 of its head group when that wave
+// starts, and wave 0 draws tickets after its own claim like every other
+// wave, so each ticket claim is drawn at least once after the zeroing and no
+// claim is skipped. A wave that draws before the zeroing is seen gets a
+// stale value: past the last ticket it stops; otherwise it streams a claim
+// that is streamed again later. A claim's partials and outputs are a function
+// of the claim's index alone, so a second streaming rewrites the same values.
+// The workspace needs no initialisation.
+//
+// Claims are numbered in list order, c = w * (1 + R) + k (k = 0: the own
+// claim), and none inside the list is empty, so the pieces of a sequence are
+// the consecutive claims from claim_of(cb) to claim_of(ce - 1). Partial slots
+// belong to claims, not sequences: a claim holds at most two partials, for
+// the sequence it starts in (slot 0: the sequence began at or before the
+// claim's first block) and for the one it ends in (slot 1: that sequence
+// began inside the claim and runs past its end), since every other sequence
+// it touches lies wholly inside it. Slot (h, c, s) is (h * bal_claims + c) *
+// 2 + s, bal_claims = P * (1 + bal_tier2), so the workspace holds
+// H * bal_claims * 2 partials whatever B and the table width.
+struct Claims {
+  int total;  // blocks in the list
+  int Lw;     // blocks per segment
+  int A;      // blocks of a segment's own claim
+  int a;      // blocks per ticket claim
+  int K;      // claims per segment, 1 + R
+};
 
-__device__ __forceinline__ int bal_blocks_per_wave(int total, int waves, int min_blocks) {
-  const int wb = (total + waves - 1) / waves;
-  return wb > min_blocks ? wb : min_blocks;
+// Same arithmetic in the attention kernel and the merge (both see the same
+// total). With bal_tier2 == 0 every wave streams its whole segment.
+__device__ __forceinline__ Claims make_claims(const DecodeArgs& a, int total) {
+  Claims c;
+  c.total = total;
+  const int64_t minb = a.bal_min_blocks;
+  int64_t Lw = ((int64_t)total + a.bal_waves - 1) / a.bal_waves;
+  if (Lw < minb) Lw = minb;
+  c.Lw = (int)Lw;  // <= max(minb, total)
+  const int64_t small = Lw * (16 - a.bal_tier1_16ths) / 16;
+  int64_t R = small / minb;
+  if (R > a.bal_tier2) R = a.bal_tier2;
+  c.a = R > 0 ? (int)(small / R) : 0;
+  c.K = 1 + (int)R;
+  c.A = (int)(Lw - R * c.a);  // >= Lw - small >= 1
+  return c;
+}
+// Claim index of list block pos (0 <= pos < total).
+__device__ __forceinline__ int claim_of(const Claims& c, int pos) {
+  const int seg = pos / c.Lw;
+  const int off = pos - seg * c.Lw;
+  return seg * c.K + (off < c.A ? 0 : 1 + (off - c.A) / c.a);
+}
+// First list block of claim i, and one past its last (empty when equal).
+__device__ __forceinline__ int claim_begin(const Claims& c, int i) {
+  const int seg = i / c.K, k = i - seg * c.K;
+  const int64_t s = (int64_t)seg * c.Lw + (k == 0 ? 0 : c.A + (int64_t)(k - 1) * c.a);
+  return (int)min(s, (int64_t)c.total);
+}
+__device__ __forceinline__ int claim_end(const Claims& c, int i) {
+  const int seg = i / c.K, k = i - seg * c.K;
+  const int64_t e = (int64_t)seg * c.Lw + c.A + (int64_t)k * c.a;
+  return (int)min(e, (int64_t)c.total);
+}
+__device__ __forceinline__ size_t bal_slot(const DecodeArgs& a, const Claims& c, int h, int i, int cb) {
+  return ((size_t)h * a.bal_claims + i) * 2 + (claim_begin(c, i) >= cb ? 0 : 1);
 }
 
 // Inclusive prefix sums of ceil(ctx_b / S) into cinc[0 .. B); returns the
@@ -425,66 +486,96 @@ paged_decode_fast_bal(const DecodeArgs a) {
   const int lane = (int)threadIdx.x;
   const int sub = lane % LPH;
   const int ngroups = (a.H + HPW - 1) / HPW;
-  const int hg = (int)blockIdx.x % ngroups;
-  const int w = (int)blockIdx.x / ngroups;
+  // Workgroups go to the 8 XCDs round-robin (workgroup id mod 8). Runs of 8
+  // consecutive workgroups share a head group, so each head group's waves,
+  // and the tickets they draw, are spread over all XCDs: wave w of head group
+  // hg runs on XCD w mod 8. (Any bijection is correct; this one balances.)
+  int hg, w;
+  {
+    const int i = (int)blockIdx.x, P = a.bal_waves;
+    const int full = ngroups * 8 * (P / 8);
+    if (i < full) {
+      const int r = i % (ngroups * 8), q = i / (ngroups * 8);
+      hg = r / 8;
+      w = q * 8 + r % 8;
+    } else {
+      hg = (i - full) % ngroups;
+      w = 8 * (P / 8) + (i - full) / ngroups;
+    }
+  }
   const int h = hg * HPW + lane / LPH;
   const bool lane_ok = FULL || (h < a.H && sub * 8 < a.D);
 
   const int total = seq_block_scan<T>(a, lane, cinc);
   if (blockIdx.x == 0)  // the merge reads the block list from the workspace
     for (int i = lane; i < a.B; i += 64) a.ws_cinc[i] = cinc[i];
-  const int wb = bal_blocks_per_wave(total, a.bal_waves, a.bal_min_blocks);
-  const int64_t first = (int64_t)w * wb;
-  if (first >= total) return;  // uniform over the wave
-  int pos = (int)first;
-  const int end = (int)min((int64_t)total, first + wb);
-
-  // The sequence holding list block pos: the first b with cinc[b] > pos.
-  int b = 0;
-  for (int lo = 0, hi = a.B - 1; lo <= hi;) {
-    const int mid = (lo + hi) >> 1;
-    if (uread(cinc, mid) > pos) {
-      b = mid;
-      hi = mid - 1;
-    } else {
-      lo = mid + 1;
-    }
-  }
+  const Claims cl = make_claims(a, total);
+  int* ticket = a.ws_ticket + hg;
+  const int n_tickets = a.bal_waves * (cl.K - 1);
+  if (n_tickets > 0 && w == 0 && lane == 0)
+    __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   uint32_t koff[Layout<T>::kLoads], voff[Layout<T>::kLoads];
   row_offsets<T>(a, h, sub, lane_ok, koff, voff);
-  // One flat loop over chunks of at most kMaxBlocksPerPart blocks of one
-  // sequence; the state is written out when the wave leaves a sequence.
-  int cb = 0, ce = 0, ctx = 0;
-  QFrag<T> q;
-  float m = -INFINITY, l = 0.f, acc[8];
-  while (pos < end) {
-    if (pos >= ce) {  // entering sequence b
-      cb = b > 0 ? uread(cinc, b - 1) : 0;
-      ce = uread(cinc, b);
-      ctx = clamp_ctx<T>(a, b);
-      load_query<T>(a, b, h, sub, lane_ok, q);
-      m = -INFINITY;
-      l = 0.f;
+
+  // Streams claim c: one flat loop over chunks of at most kMaxBlocksPerPart
+  // blocks of one sequence; the state is written out when the wave leaves a
+  // sequence.
+  auto run_claim = [&](int c) {
+    int pos = claim_begin(cl, c);
+    const int end = claim_end(cl, c);
+    if (pos >= end) return;  // uniform over the wave
+    // The sequence holding list block pos: the first b with cinc[b] > pos.
+    int b = 0;
+    for (int lo = 0, hi = a.B - 1; lo <= hi;) {
+      const int mid = (lo + hi) >> 1;
+      if (uread(cinc, mid) > pos) {
+        b = mid;
+        hi = mid - 1;
+      } else {
+        lo = mid + 1;
+      }
+    }
+    int cb = 0, ce = 0, ctx = 0;
+    QFrag<T> q;
+    float m = -INFINITY, l = 0.f, acc[8];
+    while (pos < end) {
+      if (pos >= ce) {  // entering sequence b
+        cb = b > 0 ? uread(cinc, b - 1) : 0;
+        ce = uread(cinc, b);
+        ctx = clamp_ctx<T>(a, b);
+        load_query<T>(a, b, h, sub, lane_ok, q);
+        m = -INFINITY;
+        l = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+      }
+      const int ch_end = min(min(end, ce), pos + kMaxBlocksPerPart);
+      fold_chunk<T, LPH, TOK, FULL>(a, b, lane, lane_ok, q, koff, voff, pos - cb, ch_end - cb, ctx, m, l,
+                                    acc);
+      pos = ch_end;
+      if (pos == ce || pos == end) {
+        finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, claim_of(cl, ce - 1) - claim_of(cl, cb) + 1,
+                        bal_slot(a, cl, h, c, cb));
+        // Next sequence with blocks past pos (cinc[B-1] = total bounds b while pos < end).
+        while (pos < end && uread(cinc, b) <= pos) ++b;
+      }
     }
-    const int ch_end = min(min(end, ce), pos + kMaxBlocksPerPart);
-    fold_chunk<T, LPH, TOK, FULL>(a, b, lane, lane_ok, q, koff, voff, pos - cb, ch_end - cb, ctx, m, l,
-                                  acc);
-    pos = ch_end;
-    if (pos == ce || pos == end) {
-      finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, (ce - 1) / wb - cb / wb + 1,
-                      bal_slot(a, h, w, wb, cb));
-      // Next sequence with blocks past pos (cinc[B-1] = total bounds b while pos < end).
-      while (pos < end && uread(cinc, b) <= pos) ++b;
-    }
+  };
+
+  run_claim(w * cl.K);  // this wave's own claim
+  while (n_tickets > 0) {  // then ticket claims: claim 1 + t / P of segment t % P
+    int t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    t = __builtin_amdgcn_readlane(t, 0);
+    if ((unsigned)t >= (unsigned)n_tickets) break;  // uniform over the wave
+    run_claim((t % a.bal_waves) * cl.K + 1 + t / a.bal_waves);
   }
 }
 
 // Combines the partials of every (b, h) whose context spans more than one
 // piece of work (partition mode: ceil(ctx / part_tokens) partitions;
-// balanced mode: the waves its blocks fall in). One wavefront per (sequence,
+// balanced mode: the claims its blocks fall in). One wavefront per (sequence,
 // HPW heads), the fast kernel's head grouping: in each head row, lane j loads
 // the (max, sum) of partial p0 + j while every lane loads its 8 elements of
 // all CH partial outputs of the chunk, so a chunk costs one round trip;
@@ -510,7 +601,8 @@ paged_decode_merge(const DecodeArgs a) {
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  int nparts, cb = 0, wb = 1, w_first = 0;
+  int nparts, cb = 0, c_first = 0;
+  Claims cl{};
   if (a.bal_waves > 0) {
     const int total = a.ws_cinc[a.B - 1];
     cb = b > 0 ? a.ws_cinc[b - 1] : 0;
@@ -519,9 +611,9 @@ paged_decode_merge(const DecodeArgs a) {
       if (lane_ok) store_out<T>(a, b, h, sub, acc, 0.f);
       return;
     }
-    wb = bal_blocks_per_wave(total, a.bal_waves, a.bal_min_blocks);
-    w_first = cb / wb;
-    nparts = (ce - 1) / wb - w_first + 1;
+    cl = make_claims(a, total);
+    c_first = claim_of(cl, cb);
+    nparts = claim_of(cl, ce - 1) - c_first + 1;
   } else {
     const int ctx = clamp_ctx<T>(a, b);
     nparts = (ctx + a.part_tokens - 1) / a.part_tokens;
@@ -529,7 +621,7 @@ paged_decode_merge(const DecodeArgs a) {
   if (nparts <= 1) return;  // uniform over the wave
   // Workspace slot of partial j of (b, hh).
   auto slot = [&](int j) -> size_t {
-    return a.bal_waves > 0 ? bal_slot(a, hh, w_first + j, wb, cb)
+    return a.bal_waves > 0 ? bal_slot(a, cl, hh, c_first + j, cb)
                            : ((size_t)b * a.H + hh) * a.max_parts + j;
   };
 

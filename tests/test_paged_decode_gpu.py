@@ -12,6 +12,8 @@ with NaN in every slot past a context.
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -233,11 +235,26 @@ def test_decode_microbench_invariances():
     assert torch.equal(again.view(torch.int32), base.view(torch.int32))
 
 
+# (own share in 16ths, ticket claims per wave) of the balanced split: the
+# library's default, no second tier, nearly everything by ticket, and half.
+TIERS = [None, (16, 0), (1, 16), (8, 64)]
+
+
+def _set_tiers(monkeypatch, tiers):
+    if tiers is not None:
+        monkeypatch.setenv("MINIVLLM_HIP_BAL_TIER1", str(tiers[0]))
+        monkeypatch.setenv("MINIVLLM_HIP_BAL_TIER2", str(tiers[1]))
+
+
+@pytest.mark.parametrize("tiers", TIERS)
 @pytest.mark.parametrize("B", [7, 200, 1000])
-def test_balanced_split_with_empty_and_one_token_contexts(B):
-    """The automatic split spreads every sequence's blocks evenly over the
-    waves (several sequences per wave, several waves per sequence); rows with
-    no context are zeros and one-token rows return their value row."""
+def test_balanced_split_with_empty_and_one_token_contexts(B, tiers, monkeypatch):
+    """The automatic split spreads every sequence's blocks over the waves'
+    own claims and the ticket claims (several sequences per claim, several
+    claims per sequence); rows with no context are zeros and one-token rows
+    return their value row."""
+    _set_tiers(monkeypatch, tiers)
+    print(f"  tiers={tiers}", flush=True)
     S, H, D, M = 16, 4, 64, 80
     g = torch.Generator().manual_seed(B)
     choices = torch.tensor([0, 1, 2, 15, 16, 17, 300, 1000, M * S])
@@ -253,6 +270,53 @@ def test_balanced_split_with_empty_and_one_token_contexts(B):
     want = c_oracle.paged_decode(*oracle_args(q, pool, tables, lens, layer))
     np.testing.assert_allclose(got, want, **F32_TOL)
     assert (got[ctx.numpy() == 0] == 0).all()
+
+
+@pytest.mark.parametrize("tiers", [None, (1, 16)])
+def test_balanced_split_ignores_stale_workspace(tiers, monkeypatch):
+    """The workspace is used as found: NaN bytes, zeros, or ticket counters
+    left at 1 give the same output, bit for bit, as a fresh workspace."""
+    _set_tiers(monkeypatch, tiers)
+    print(f"  stale workspace tiers={tiers} B=64 H=32 D=128 bf16 ctx U[512,1024]", flush=True)
+    w = fx.make_decode_workload(64, 32, 128, 16, 5000, 512, 1024, torch.bfloat16, DEV, seed=3,
+                                poison=False, table_width=64)
+    lib = hpd._native.lib()
+    B, H, D = w.q.shape
+    L, N, S = w.pool.k.shape[:3]
+    M = w.tables.shape[1]
+    assert lib.mgi_paged_decode_balanced_waves(B, H, D, S, M, 0) > 0
+    ws_bytes = int(lib.mgi_paged_decode_workspace_bytes(B, H, D, S, M, 0))
+
+    def call(ws):
+        out = torch.empty_like(w.q)
+        st = lib.mgi_paged_decode(
+            out.data_ptr(), hpd._native.strides(out), w.q.data_ptr(), hpd._native.strides(w.q),
+            w.pool.k.data_ptr(), w.pool.v.data_ptr(), hpd._native.strides(w.pool.k),
+            hpd._native.strides(w.pool.v), hpd._native.DTYPE_CODES[w.q.dtype],
+            w.tables.data_ptr(), hpd._native.strides(w.tables), hpd._native.ITYPE_CODES[w.tables.dtype],
+            w.ctx.data_ptr(), w.ctx.stride(0), hpd._native.ITYPE_CODES[w.ctx.dtype],
+            B, H, D, S, N, M, L, int(w.layer), 1.0 / math.sqrt(D), 0, ws.data_ptr(), ws_bytes,
+            hpd._native.stream_handle(DEV))
+        hpd._native.check(st)
+        torch.cuda.synchronize()
+        return out
+
+    base = hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer)
+    torch.cuda.synchronize()
+    assert torch.isfinite(base.float()).all()
+    n_groups = H // 4
+    for name in ("nan", "zero", "one"):
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+        if name == "nan":
+            ws.fill_(0xFF)
+        elif name == "zero":
+            ws.zero_()
+        else:
+            ws.fill_(0xFF)
+            ws[ws_bytes - 4 * n_groups:].view(torch.int32).fill_(1)
+        for rep in range(2):  # the second call finds the first call's counters
+            got = call(ws)
+            assert torch.equal(got.view(torch.int16), base.view(torch.int16)), (name, rep)
 
 
 def test_long_context_split_decode():
