@@ -15,7 +15,8 @@ reference's online-softmax decode (oracle/paged_decode_oracle.c, fp32
 accumulation) on this host's cores over the same workload.
 
 Extras (skipped with --no-extras) time other decode shapes, the KV append,
-the paged prefill kernel and same-GPU comparisons with the PyTorch backends.
+the KV append plus decode attention of one high-batch step on one pool, the
+paged prefill kernel and same-GPU comparisons with the PyTorch backends.
 The end-to-end block (skipped with --no-e2e) runs the full runtime under
 recompute preemption and puts its decode tokens/s in `end_to_end`.
 
@@ -123,6 +124,59 @@ def append_line(steps, warmup, dev):
     nbytes = n_valid * H * D * 2 * 2 * 2 + B * 8
     return {"us": round(ms * 1e3, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "valid_rows": n_valid,
             "alg_bytes": nbytes, "note": "launch-latency bound; working set is cache resident"}
+
+
+def c3_step_line(steps, warmup, dev):
+    """One high-batch decode step of one layer as the KV-append-plus-decode
+    configuration states it: B=256, H=32, D=128, bf16, ctx ~ U[128, 2048],
+    a 32768-block pool allocated from a seeded permutation. Each row's new
+    token is appended at slot table[ctx // 16] * 16 + ctx % 16 (a fresh block
+    when ctx % 16 == 0), 10 % of the rows are padding (slot -1), then decode
+    attention runs over ctx + 1 tokens for appended rows and ctx for padded
+    ones. The append and the attention are timed together, on one pool."""
+    import torch
+
+    import _fixtures as fx
+    from minivllm import hip_paged_decode as hpd
+    from minivllm.kv_block_pool import KVBlockPool
+
+    B, H, D, S, N = 256, 32, 128, 16, 32768
+    g = torch.Generator().manual_seed(0)
+    ctx = torch.randint(128, 2049, (B,), generator=g, dtype=torch.int64)
+    pad = torch.zeros(B, dtype=torch.bool)
+    pad[torch.randperm(B, generator=g)[: B // 10]] = True
+    lens = torch.where(pad, ctx, ctx + 1)
+    nblk = (lens + S - 1) // S
+    M = int(nblk.max())
+    perm = torch.randperm(N, generator=g)
+    tables = torch.full((B, M), -1, dtype=torch.int64)
+    starts = torch.cumsum(nblk, 0) - nblk
+    for b in range(B):
+        tables[b, : nblk[b]] = perm[starts[b]: starts[b] + nblk[b]]
+    col = torch.clamp(ctx // S, max=M - 1)
+    slots = torch.where(pad, torch.full_like(ctx, -1), tables[torch.arange(B), col] * S + ctx % S)
+    assert bool((slots[~pad] >= 0).all())
+    pool = KVBlockPool(1, N, S, H, D, device=dev, dtype=torch.bfloat16)
+    gd = torch.Generator(device=dev).manual_seed(1)
+    for t in (pool.k, pool.v):
+        t.normal_(generator=gd)
+    q = torch.randn((B, H, D), generator=gd, device=dev).to(torch.bfloat16)
+    k_new = torch.randn((B, H, D), generator=gd, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((B, H, D), generator=gd, device=dev).to(torch.bfloat16)
+    tables_d, lens_d, slots_d = tables.to(dev), lens.to(dev), slots.to(dev)
+
+    def step():
+        hpd.kv_append(pool, 0, k_new, v_new, slots_d)
+        hpd.paged_attention_batch_hip(q, pool, tables_d, lens_d, 0)
+
+    ms = time_steps(step, steps, warmup)
+    n_valid = int((~pad).sum())
+    append_bytes = n_valid * H * D * 2 * 2 * 2 + B * 8
+    attn_bytes = fx.DecodeWorkload(q, pool, tables_d, lens_d, 0, {}).algorithmic_bytes()
+    gbps = (append_bytes + attn_bytes) / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 2), "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+            "append_bytes": append_bytes, "attention_bytes": attn_bytes, "valid_rows": n_valid,
+            "sum_ctx": int(lens.sum()), "rows_per_s_per_layer": round(B / (ms * 1e-3), 1)}
 
 
 def copy_line(mib: int, dev, reps: int = 3):
@@ -577,6 +631,8 @@ def main() -> None:
             log(f"extra B256: {extras['decode_bf16_B256_ctx128-2048']}")
             extras["kv_append_bf16_B256"] = append_line(max(20, args.steps), 5, dev)
             log(f"extra append: {extras['kv_append_bf16_B256']}")
+            extras["append_plus_decode_bf16_B256_ctx128-2048"] = c3_step_line(max(10, args.steps // 2), 3, dev)
+            log(f"extra append+decode: {extras['append_plus_decode_bf16_B256_ctx128-2048']}")
             extras["d2d_copy_4GiB"] = copy_line(4096, dev, reps=5)
             log(f"extra copy: {extras['d2d_copy_4GiB']}")
             torch.cuda.empty_cache()
