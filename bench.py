@@ -629,6 +629,17 @@ def main() -> None:
             extras["decode_bf16_B256_ctx128-2048"] = decode_line(w5, max(5, args.steps // 2), 3, 0)
             del w5
             log(f"extra B256: {extras['decode_bf16_B256_ctx128-2048']}")
+            # One GPU's share of an 8-way head split (tensor parallel): the same
+            # batches and contexts with 32 / 8 = 4 heads.
+            w6 = fx.make_decode_workload(B, 4, D, S, N, 512, 4096, torch.bfloat16, dev, seed=0, poison=False)
+            extras["tp8_shard_decode_bf16_H4_ctx512-4096"] = decode_line(w6, max(10, args.steps), 5, 0)
+            del w6
+            log(f"extra tp8 shard: {extras['tp8_shard_decode_bf16_H4_ctx512-4096']}")
+            w7 = fx.make_decode_workload(8, 4, D, S, 65536, 32768, 131072, torch.bfloat16, dev, seed=0,
+                                         poison=False)
+            extras["tp8_shard_longctx_bf16_B8_H4_ctx32k-128k"] = decode_line(w7, max(10, args.steps // 2), 3, 0)
+            del w7
+            log(f"extra tp8 shard long: {extras['tp8_shard_longctx_bf16_B8_H4_ctx32k-128k']}")
             extras["kv_append_bf16_B256"] = append_line(max(20, args.steps), 5, dev)
             log(f"extra append: {extras['kv_append_bf16_B256']}")
             extras["append_plus_decode_bf16_B256_ctx128-2048"] = c3_step_line(max(10, args.steps // 2), 3, dev)

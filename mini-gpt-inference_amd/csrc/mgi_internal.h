@@ -35,6 +35,7 @@ struct DecodeArgs {
   int bal_tier1_16ths;// balanced mode: share of each segment in its wave's own claim (16ths)
   int bal_tier2;      // balanced mode: ticket claims per segment, at most (0: none)
   int bal_claims;     // balanced mode: bal_waves * (1 + bal_tier2), partial slot pairs per head
+  int merge_waves;    // wavefronts per workgroup of paged_decode_merge (1, 2, 4 or 8)
   float* ws_acc;      // [B, H, max_parts, D] unnormalised partial outputs
   float2* ws_ml;      // [B, H, max_parts]    partial (max, sum), log2 domain
   int* ws_cinc;       // balanced mode: [B] inclusive prefix sums of blocks per sequence

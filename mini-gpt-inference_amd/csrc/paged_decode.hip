@@ -584,12 +584,17 @@ paged_decode_fast_bal(const DecodeArgs a) {
 //   O' = O 2^(M-M') + sum_j O_j 2^(m_j-M').
 // In balanced mode it also writes the zero output of a sequence with no
 // blocks, which no attention wave visits.
-template <typename T, int LPH>
-__global__ void __launch_bounds__(64)
+//
+// With MW > 1 wavefronts per workgroup (small grids, where each (sequence,
+// head group) has many partials), wavefront w folds chunks w, w + MW, ... and
+// wavefront 0 combines the MW states through LDS with the same recurrence.
+template <typename T, int LPH, int MW>
+__global__ void __launch_bounds__(64 * MW)
 paged_decode_merge(const DecodeArgs a) {
   constexpr int HPW = 64 / LPH;
   constexpr int CH = LPH < 16 ? LPH : 16;  // partials per chunk
-  const int lane = (int)threadIdx.x;
+  const int lane = (int)threadIdx.x & 63;
+  const int wv = (int)threadIdx.x >> 6;
   const int sub = lane % LPH;
   const int row = lane / LPH;
   const int b = (int)blockIdx.y;
@@ -608,7 +613,7 @@ paged_decode_merge(const DecodeArgs a) {
     cb = b > 0 ? a.ws_cinc[b - 1] : 0;
     const int ce = a.ws_cinc[b];
     if (ce <= cb) {  // no blocks: zeros, as for an empty context
-      if (lane_ok) store_out<T>(a, b, h, sub, acc, 0.f);
+      if (lane_ok && wv == 0) store_out<T>(a, b, h, sub, acc, 0.f);
       return;
     }
     cl = make_claims(a, total);
@@ -626,7 +631,7 @@ paged_decode_merge(const DecodeArgs a) {
   };
 
   float M = -INFINITY, L = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += CH) {
+  for (int p0 = wv * CH; p0 < nparts; p0 += MW * CH) {
     float2 ml = make_float2(-INFINITY, 0.f);
     if (head_ok && sub < CH && p0 + sub < nparts) ml = a.ws_ml[slot(p0 + sub)];
     float4 x0[CH], x1[CH];
@@ -659,6 +664,31 @@ paged_decode_merge(const DecodeArgs a) {
       acc[7] = fmaf(wj, x1[j].w, acc[7]);
     }
     M = Mn;
+  }
+  if constexpr (MW > 1) {
+    // Combine the wavefronts' states: M = max_w M_w, L = sum_w L_w 2^(M_w - M),
+    // O = sum_w O_w 2^(M_w - M). A wavefront with no chunk has M_w = -inf.
+    __shared__ float st_m[MW][64], st_l[MW][64], st_o[MW][8][64];
+    st_m[wv][lane] = M;
+    st_l[wv][lane] = L;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st_o[wv][i][lane] = acc[i];
+    __syncthreads();
+    if (wv != 0) return;
+    M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < MW; ++w) M = fmaxf(M, st_m[w][lane]);
+    L = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int w = 0; w < MW; ++w) {
+      const float mw = st_m[w][lane];
+      const float f = mw == -INFINITY ? 0.f : fast_exp2(mw - M);
+      L = fmaf(f, st_l[w][lane], L);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = fmaf(f, st_o[w][i][lane], acc[i]);
+    }
   }
   if (!lane_ok) return;
   store_out<T>(a, b, h, sub, acc, L > 0.f ? 1.f / L : 0.f);
@@ -753,8 +783,13 @@ static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_
     e = launch(fn, dim3(ngroups, (unsigned)a.max_parts, (unsigned)a.B), dim3(64), a, stream);
   }
   if (e != hipSuccess || (a.bal_waves <= 0 && a.max_parts <= 1)) return e;
-  return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH>), dim3(ngroups, (unsigned)a.B),
-                dim3(64), a, stream);
+  const dim3 mgrid(ngroups, (unsigned)a.B);
+  switch (a.merge_waves) {
+    case 8: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 8>), mgrid, dim3(512), a, stream);
+    case 4: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 4>), mgrid, dim3(256), a, stream);
+    case 2: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 2>), mgrid, dim3(128), a, stream);
+    default: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 1>), mgrid, dim3(64), a, stream);
+  }
 }
 
 template <typename T, int LPH>
