@@ -8,4 +8,4 @@ for p in (str(ROOT / "mini-gpt-inference_amd"), str(ROOT), str(Path(__file__).re
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (run on the GPU box)")
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU")
