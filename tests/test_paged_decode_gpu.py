@@ -319,6 +319,19 @@ def test_balanced_split_ignores_stale_workspace(tiers, monkeypatch):
             assert torch.equal(got.view(torch.int16), base.view(torch.int16)), (name, rep)
 
 
+@pytest.mark.parametrize("split", [0, 256], ids=["auto", "partitions"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_few_sequences_many_partials(dtype, split):
+    """Few (sequence, head group) pairs with many partials each: the merge
+    runs several wavefronts per workgroup (B=3, 4 heads, contexts of 5k-12k
+    tokens split over hundreds of claims or 256-token partitions)."""
+    ctx = [5001, 12000, 7777]
+    q, pool, tables, lens, layer = _small_case(3, 4, 128, 16, ctx, dtype, seed=31)
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer, split_tokens=split)
+    want = c_oracle.paged_decode(*oracle_args(q, pool, tables, lens, layer))
+    np.testing.assert_allclose(got, want, **tol_for(dtype))
+
+
 def test_long_context_split_decode():
     """B=8, H=32, D=128, bf16, ctx ~ U[32768, 131072] over a 65536-block pool."""
     print("  workload B=8 ctx U[32768,131072] N=65536 bf16", flush=True)
