@@ -278,3 +278,24 @@ def test_workgroup_map_is_a_bijection_spreading_head_groups_over_xcds(ngroups, P
     for g in range(ngroups):
         xcds = [i % 8 for i in range(ngroups * P) if seen[i][0] == g and seen[i][1] < 8 * (P // 8)]
         assert all(xcds.count(x) == P // 8 for x in range(8))
+
+
+def test_tier_overrides_are_clamped_and_size_the_workspace(monkeypatch):
+    lib = _native.lib()
+    B, H, D, S, M = 64, 32, 128, 16, 256
+    waves = lib.mgi_paged_decode_balanced_waves(B, H, D, S, M, 0)
+
+    def expected(r):
+        n = H * waves * (1 + r) * 2
+        ml = math.ceil(n * D * 4 / 256) * 256
+        return math.ceil((ml + n * 8) / 256) * 256 + B * 4 + (H // 4) * 4
+
+    for r_env, r in (("0", 0), ("3", 3), ("100", 64), ("-5", 0)):
+        monkeypatch.setenv("MINIVLLM_HIP_BAL_TIER2", r_env)
+        assert lib.mgi_paged_decode_workspace_bytes(B, H, D, S, M, 0) == expected(r), r_env
+    monkeypatch.delenv("MINIVLLM_HIP_BAL_TIER2")
+    assert lib.mgi_paged_decode_workspace_bytes(B, H, D, S, M, 0) == expected(3)   # the default
+    # the own-claim share only changes how segments are cut, not the workspace
+    for t1 in ("0", "16", "99"):
+        monkeypatch.setenv("MINIVLLM_HIP_BAL_TIER1", t1)
+        assert lib.mgi_paged_decode_workspace_bytes(B, H, D, S, M, 0) == expected(3)
