@@ -42,6 +42,13 @@ for _p in (str(ROOT / "mini-gpt-inference_amd"), str(ROOT), str(ROOT / "tests"))
 
 METRIC = "paged decode attn HBM GB/s (% of peak) + decode tokens/s, 1 MI355X"
 PEAK_GBPS = 8000.0
+# Main-line decode shapes: name -> (B, pool blocks, ctx low, ctx high, description); 32 heads,
+# head_dim 128, block_size 16, seed 0.
+WORKLOADS = {
+    "microbench": (64, 20000, 512, 4096, "paged decode attention microbench (one layer, one decode step)"),
+    "longctx": (8, 65536, 32768, 131072, "paged decode attention, long contexts (one layer, one decode step)"),
+    "b256": (256, 32768, 128, 2048, "paged decode attention, high batch (one layer, one decode step)"),
+}
 
 
 def parse_args():
@@ -51,6 +58,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--dtype", choices=("bf16", "fp32"), default="bf16")
     ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--workload", choices=tuple(WORKLOADS), default="microbench",
+                    help="decode shape of the main line (default: the microbench; the others are the "
+                         "long-context and high-batch shapes of the extras, for profiling)")
     ap.add_argument("--no-extras", action="store_true", help="skip the other workload shapes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-e2e", action="store_true",
@@ -586,11 +596,12 @@ def main() -> None:
             print(json.dumps(e2e_trace_line(args.e2e_requests, dev)), flush=True)
         return
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float32
-    B, H, D, S, N = 64, 32, 128, 16, 20000
+    B, N, ctx_lo, ctx_hi, wl_desc = WORKLOADS[args.workload]
+    H, D, S = 32, 128, 16
 
     with torch.inference_mode():
-        log(f"building decode workload B={B} H={H} D={D} S={S} N={N} ctx U[512,4096] {args.dtype}")
-        w = fx.make_decode_workload(B, H, D, S, N, 512, 4096, dtype, dev, seed=0, poison=False)
+        log(f"building decode workload B={B} H={H} D={D} S={S} N={N} ctx U[{ctx_lo},{ctx_hi}] {args.dtype}")
+        w = fx.make_decode_workload(B, H, D, S, N, ctx_lo, ctx_hi, dtype, dev, seed=0, poison=False)
         from minivllm import _native
 
         M = w.tables.shape[1]
@@ -609,11 +620,11 @@ def main() -> None:
         if not args.no_extras:
             other = torch.float32 if dtype == torch.bfloat16 else torch.bfloat16
             tag = "fp32" if other == torch.float32 else "bf16"
-            w2 = fx.make_decode_workload(B, H, D, S, N, 512, 4096, other, dev, seed=0, poison=False)
+            w2 = fx.make_decode_workload(64, H, D, S, 20000, 512, 4096, other, dev, seed=0, poison=False)
             extras[f"decode_{tag}"] = decode_line(w2, max(5, args.steps // 2), 3, args.split_tokens)
             del w2
             log(f"extra decode_{tag}: {extras[f'decode_{tag}']}")
-            w3 = fx.make_decode_workload(B, H, D, S, 20000, 4096, 4096, dtype, dev, seed=0,
+            w3 = fx.make_decode_workload(64, H, D, S, 20000, 4096, 4096, dtype, dev, seed=0,
                                          fixed_ctx=4096, poison=False)
             extras[f"decode_{args.dtype}_ctx4096"] = decode_line(w3, max(5, args.steps // 2), 3,
                                                                   args.split_tokens)
@@ -631,7 +642,7 @@ def main() -> None:
             log(f"extra B256: {extras['decode_bf16_B256_ctx128-2048']}")
             # One GPU's share of an 8-way head split (tensor parallel): the same
             # batches and contexts with 32 / 8 = 4 heads.
-            w6 = fx.make_decode_workload(B, 4, D, S, N, 512, 4096, torch.bfloat16, dev, seed=0, poison=False)
+            w6 = fx.make_decode_workload(64, 4, D, S, 20000, 512, 4096, torch.bfloat16, dev, seed=0, poison=False)
             extras["tp8_shard_decode_bf16_H4_ctx512-4096"] = decode_line(w6, max(10, args.steps), 5, 0)
             del w6
             log(f"extra tp8 shard: {extras['tp8_shard_decode_bf16_H4_ctx512-4096']}")
@@ -714,7 +725,7 @@ def main() -> None:
             cpu["prefill"] = cpu_prefill_baseline()
             log(f"cpu: {cpu}")
 
-    workload_tag = f"decode_microbench_{args.dtype}_B{B}_H{H}_D{D}_ctx512-4096"
+    workload_tag = f"decode_{args.workload}_{args.dtype}_B{B}_H{H}_D{D}_ctx{ctx_lo}-{ctx_hi}"
     traffic, traffic_src = profiled_traffic(workload_tag, split)
     result = {
         "metric": METRIC,
@@ -729,9 +740,9 @@ def main() -> None:
         "vs_baseline": None,
         "dtype": args.dtype,
         "data": "synthetic: seeded N(0,1) q/K/V, contexts and a random block permutation (seed 0)",
-        "config": {"workload": "paged decode attention microbench (one layer, one decode step)",
+        "config": {"workload": wl_desc,
                    "batch": B, "heads": H, "head_dim": D, "block_size": S, "pool_blocks": N,
-                   "ctx": "U[512,4096]", "sum_ctx": main_line["sum_ctx"], "split": split},
+                   "ctx": f"U[{ctx_lo},{ctx_hi}]", "sum_ctx": main_line["sum_ctx"], "split": split},
         "pct_of_peak": main_line["pct_of_peak"],
         "decode_seq_per_s_per_layer": main_line["seq_per_s_per_layer"],
         "end_to_end": e2e_summary,
