@@ -325,7 +325,8 @@ def prefill_line(dev, start: int, T: int, H: int = 16, D: int = 128, steps: int 
     sdpa_ms = time_steps(lambda: attn._dense_prefill(q, k, v, start, pool, seq, 0), max(3, steps // 4), 1)
     flops = 4 * H * D * (T * start + T * (T + 1) // 2)
     tflops = flops / (hip_ms * 1e-3) / 1e12
-    return {"start": start, "T": T, "H": H, "D": D, "us": round(hip_ms * 1e3, 2),
+    split = hpd._native.lib().mgi_paged_prefill_workspace_bytes(start, T, H, D, hpd._native.DTYPE_CODES[q.dtype]) > 0
+    return {"start": start, "T": T, "H": H, "D": D, "key_split": bool(split), "us": round(hip_ms * 1e3, 2),
             "tflops": round(tflops, 1), "pct_of_bf16_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
             "sdpa_v2_fp32_us": round(sdpa_ms * 1e3, 1), "speedup_vs_sdpa_v2": round(sdpa_ms / hip_ms, 1)}
 
@@ -666,7 +667,7 @@ def main() -> None:
             torch.cuda.empty_cache()
 
         if not args.no_extras or not args.no_e2e or args.prefill:
-            for start, T in ((0, 512), (2048, 2048)):
+            for start, T in ((0, 512), (2048, 2048), (4096, 256)):
                 key = f"prefill_bf16_start{start}_T{T}_H16_D128"
                 extras[key] = prefill_line(dev, start, T)
                 log(f"extra {key}: {extras[key]}")

@@ -58,7 +58,9 @@ enum mgi_itype { MGI_I32 = 0, MGI_I64 = 1 };
 const char* mgi_last_error(void);
 
 /* ABI version of this library (major*100 + minor). 1.01 added
- * mgi_paged_decode_balanced_waves and the even split of split_tokens = 0. */
+ * mgi_paged_decode_balanced_waves and the even split of split_tokens = 0;
+ * 1.02 the prefill key split (mgi_paged_prefill's workspace arguments and
+ * mgi_paged_prefill_workspace_bytes). */
 int mgi_abi_version(void);
 
 /*
@@ -180,6 +182,12 @@ int64_t mgi_paged_decode_balanced_waves(int64_t B, int64_t H, int64_t D,
  * on the bf16 matrix cores with P rounded to bf16 for the PV product).
  * Layouts: q, out [T, H, D] (any strides); block_table [n_blocks] with
  * element stride bt_stride.
+ * A chunk too small to fill the GPU (2-byte types) has its keys split over
+ * several workgroups per query tile and the partials merged in a second
+ * pass; workspace must then hold mgi_paged_prefill_workspace_bytes(...)
+ * bytes for the same (start_pos, T, H, D, dtype). It may be NULL when that
+ * is 0. Its contents need no initialisation; calls that overlap in time
+ * need separate workspaces. (ABI 1.02 added workspace, workspace_bytes.)
  */
 int mgi_paged_prefill(void* out, const int64_t* out_strides, /* [3] */
                       const void* q, const int64_t* q_strides, /* [3] */
@@ -191,7 +199,15 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, /* [3] */
                       int64_t n_blocks, int64_t start_pos, int64_t T,
                       int64_t H, int64_t D, int64_t S, int64_t N,
                       int64_t L, int64_t layer_idx, float scale,
+                      void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/* Workspace bytes mgi_paged_prefill needs for these sizes on the current
+ * device (0 if it does not split the keys). No counterpart in the
+ * reference: it sizes the workspace of the split, as
+ * mgi_paged_decode_workspace_bytes does for decode. */
+size_t mgi_paged_prefill_workspace_bytes(int64_t start_pos, int64_t T,
+                                         int64_t H, int64_t D, int dtype);
 
 #ifdef __cplusplus
 }

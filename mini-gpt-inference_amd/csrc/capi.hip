@@ -190,13 +190,83 @@ int next_pow2_at_least4(int64_t x) {
   return p;
 }
 
+// Rows of a chunk at contexts start+1 .. start+T whose keys span several
+// partitions of pk keys, counted once per partition they span.
+int64_t split_partials(int64_t start, int64_t T, int64_t pk) {
+  int64_t n = 0;
+  for (int64_t j = 2; (j - 1) * pk < start + T; ++j) {
+    const int64_t lo = std::max(start + 1, (j - 1) * pk + 1), hi = std::min(start + T, j * pk);
+    if (hi >= lo) n += (hi - lo + 1) * j;
+  }
+  return n;
+}
+
+// Paged prefill key split: keys per partition, or 0 for none. A chunk whose
+// workgroups (one per 64-row query tile and head, 32 rows for chunks of at
+// most 32) are fewer than two per CU leaves CUs idle and waits on its last
+// query tile, which folds every key tile of the prefix. Splitting each query
+// tile's keys into partitions of k tiles, k about the total key tiles over
+// two per CU (at least 2), spreads that work; the partials are combined by
+// paged_decode_merge. The split is taken when a cost model fitted on MI355X
+// (bf16, head_dim 128, 8-32 heads, chunks of 64-2048 rows after prefixes of
+// 0-16k tokens) says it pays: a lone workgroup takes ~1.5 us per 64-key
+// tile (scaled with head_dim), and the split adds ~8 us (merge launch, tail)
+// plus its fp32 partials written and read back at ~5 TB/s. It pays after
+// long prefixes (a 256-row chunk after 3000 tokens, 32 heads: 80 -> 41 us)
+// and not for chunks whose causal triangle is most of the work (a 512-row
+// chunk at position 0: 18 -> 26 us split). 2-byte types with head_dim a
+// multiple of 8 only (the merge's lane layout).
+// MINIVLLM_HIP_PREFILL_SPLIT_KEYS = -1 turns it off; > 0 forces that many
+// keys per partition, rounded up to 64, without the cost model (tuning and
+// tests; read on every call).
+int64_t prefill_split_keys(int64_t start, int64_t T, int64_t H, int64_t D, int dtype) {
+  const int forced = env_int("MINIVLLM_HIP_PREFILL_SPLIT_KEYS", 0);
+  if (forced < 0 || dtype == MGI_F32 || D % 8 != 0 || mgi::prefill_head_dim_bucket(1, (int)D) == 0 ||
+      T <= 0 || T > kMaxGridYZ)
+    return 0;
+  const int64_t QB = T <= 32 ? 32 : 64;
+  const int64_t nq = (T + QB - 1) / QB;
+  int64_t total = 0, longest = 0;
+  for (int64_t qt = 0; qt < nq; ++qt) {
+    const int64_t tiles = (start + std::min(T, (qt + 1) * QB) + 63) / 64;
+    total += tiles;
+    longest = std::max(longest, tiles);
+  }
+  if (forced > 0) return round_up(forced, 64) < longest * 64 ? round_up(forced, 64) : 0;
+  const int64_t slots = 2 * (int64_t)device_cus();
+  if (nq * H >= slots) return 0;
+  const int64_t k = std::max<int64_t>(2, (total * H + slots - 1) / slots);
+  if (k >= longest) return 0;
+  const double tile_us = 1.5 * (double)std::max<int64_t>(D, 64) / 128.0;
+  const double partial_bytes = (double)split_partials(start, T, 64 * k) * (double)H * (double)(4 * D + 8);
+  const double split_us = (double)k * tile_us + 8.0 + 2.0 * partial_bytes / 5.0e6;
+  return split_us < (double)longest * tile_us ? 64 * k : 0;
+}
+
+struct PrefillWorkspace {
+  int64_t part_keys, max_parts;
+  size_t ml_offset, total;
+};
+
+// [acc: T*H*max_parts*D f32 | ml: T*H*max_parts float2], 256-byte aligned.
+PrefillWorkspace prefill_workspace(int64_t start, int64_t T, int64_t H, int64_t D, int dtype) {
+  PrefillWorkspace w{};
+  w.part_keys = prefill_split_keys(start, T, H, D, dtype);
+  if (w.part_keys == 0) return w;
+  w.max_parts = (start + T + w.part_keys - 1) / w.part_keys;
+  const int64_t n = T * H * w.max_parts;
+  w.ml_offset = (size_t)round_up(n * D * 4, kWorkspaceAlign);
+  w.total = w.ml_offset + (size_t)(n * 8);
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* mgi_last_error(void) { return g_err.c_str(); }
 
-int mgi_abi_version(void) { return 101; }
+int mgi_abi_version(void) { return 102; }
 
 int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                       int64_t split_tokens) {
@@ -208,6 +278,11 @@ int64_t mgi_paged_decode_balanced_waves(int64_t B, int64_t H, int64_t D, int64_t
                                         int64_t split_tokens) {
   if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || M <= 0) return 0;
   return split_plan(B, H, D, S, M, split_tokens).bal_waves;
+}
+
+size_t mgi_paged_prefill_workspace_bytes(int64_t start_pos, int64_t T, int64_t H, int64_t D, int dtype) {
+  if (start_pos < 0 || T <= 0 || H <= 0 || D <= 0 || !valid_dtype(dtype)) return 0;
+  return prefill_workspace(start_pos, T, H, D, dtype).total;
 }
 
 size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
@@ -433,7 +508,8 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
                       const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
                       const void* block_table, int64_t bt_stride, int bt_itype, int64_t n_blocks,
                       int64_t start_pos, int64_t T, int64_t H, int64_t D, int64_t S, int64_t N,
-                      int64_t L, int64_t layer_idx, float scale, void* stream) {
+                      int64_t L, int64_t layer_idx, float scale, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   using namespace mgi;
   g_err.clear();
   if (T < 0) return fail(MGI_EINVAL, "row count must be non-negative");
@@ -510,7 +586,44 @@ int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,
     // bf16 chunk of 16 heads, as each thread then stages twice the tile.)
     a.cus = device_cus();
     const int waves = T <= 32 ? 2 : 4;
+    const PrefillWorkspace pw = prefill_workspace(start_pos, T, H, D, dtype);
+    if (pw.part_keys > 0) {
+      if (!workspace) return fail(MGI_EWORKSPACE, "workspace required for the split-key pass");
+      if (workspace_bytes < pw.total)
+        return fail(MGI_EWORKSPACE, "workspace smaller than mgi_paged_prefill_workspace_bytes()");
+      if (!aligned16(workspace)) return fail(MGI_EINVAL, "workspace must be 16-byte aligned");
+      a.part_keys = (int)pw.part_keys;
+      a.max_parts = (int)pw.max_parts;
+      a.ws_acc = static_cast<float*>(workspace);
+      a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + pw.ml_offset);
+    }
     e = launch_paged_prefill(a, dtype, dp, waves, 1, st);
+    if (e == hipSuccess && pw.part_keys > 0) {
+      // Rows whose keys span several partitions: the decode merge in
+      // partition mode, row i at context start_pos + i + 1.
+      DecodeArgs m{};
+      m.out = out;
+      m.o_sb = out_strides[0];
+      m.o_sh = out_strides[1];
+      m.o_sd = out_strides[2];
+      m.cl = nullptr;
+      m.ctx_base = start_pos;
+      m.B = (int)T;
+      m.H = (int)H;
+      m.D = (int)D;
+      m.S = (int)S;
+      m.M = (int)((start_pos + T + S - 1) / S);
+      m.N = N;
+      m.part_tokens = (int)pw.part_keys;
+      m.max_parts = (int)pw.max_parts;
+      m.ws_acc = a.ws_acc;
+      m.ws_ml = a.ws_ml;
+      const int lph = next_pow2_at_least4(D / 8);
+      const int64_t groups = (H + 64 / lph - 1) / (64 / lph);
+      m.merge_waves = 1;
+      while (m.merge_waves < 8 && T * groups * m.merge_waves < 2 * (int64_t)device_cus()) m.merge_waves *= 2;
+      e = launch_paged_merge(m, dtype, lph, st);
+    }
   } else {
     // Any other shape: the chunk as T single-query rows of the generic decode
     // kernel, sharing one table row, with context lengths start_pos + t + 1.

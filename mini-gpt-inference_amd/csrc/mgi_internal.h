@@ -81,6 +81,10 @@ struct PrefillArgs {
   float scale_log2;   // softmax scale * log2(e)
   int pair_round;     // > 0: workgroups per XCD in one slot round (see the kernel's grid mapping)
   int cus;            // compute units of the device (set by the caller)
+  int part_keys;      // > 0: keys per partition (a multiple of 64) when the keys are split
+  int max_parts;      // split keys: partitions per row the workspace holds
+  float* ws_acc;      // split keys: [T, H, max_parts, D] unnormalised partial outputs
+  float2* ws_ml;      // split keys: [T, H, max_parts] partial (max, sum), log2 domain
 };
 
 // Largest batch of the fast decode kernel's balanced mode (its per-wave
@@ -107,6 +111,10 @@ hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan&
 int prefill_head_dim_bucket(int two_byte, int D);
 hipError_t launch_paged_prefill(const PrefillArgs& a, int dtype, int dp, int waves, int qpw,
                                 hipStream_t stream);
+
+// paged_decode_merge alone (partition mode), for partials another kernel wrote
+// in its layout; `lanes_per_head` as in DecodePlan.
+hipError_t launch_paged_merge(const DecodeArgs& a, int dtype, int lanes_per_head, hipStream_t stream);
 
 // KV append launchers. `vector_path` copies 16-byte chunks (same dtype,
 // contiguous aligned rows); otherwise an element loop converts dtypes.

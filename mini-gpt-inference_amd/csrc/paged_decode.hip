@@ -768,6 +768,18 @@ static hipError_t launch(const void* fn, dim3 grid, dim3 block, const DecodeArgs
   return hipLaunchKernel(fn, grid, block, args, 0, stream);
 }
 
+template <typename T, int LPH>
+static hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
+  constexpr int HPW = 64 / LPH;
+  const dim3 mgrid((unsigned)((a.H + HPW - 1) / HPW), (unsigned)a.B);
+  switch (a.merge_waves) {
+    case 8: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 8>), mgrid, dim3(512), a, stream);
+    case 4: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 4>), mgrid, dim3(256), a, stream);
+    case 2: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 2>), mgrid, dim3(128), a, stream);
+    default: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 1>), mgrid, dim3(64), a, stream);
+  }
+}
+
 template <typename T, int LPH, int TOK>
 static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_t stream) {
   constexpr int HPW = 64 / LPH;
@@ -783,13 +795,7 @@ static hipError_t launch_fast_lph_tok(const DecodeArgs& a, bool full, hipStream_
     e = launch(fn, dim3(ngroups, (unsigned)a.max_parts, (unsigned)a.B), dim3(64), a, stream);
   }
   if (e != hipSuccess || (a.bal_waves <= 0 && a.max_parts <= 1)) return e;
-  const dim3 mgrid(ngroups, (unsigned)a.B);
-  switch (a.merge_waves) {
-    case 8: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 8>), mgrid, dim3(512), a, stream);
-    case 4: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 4>), mgrid, dim3(256), a, stream);
-    case 2: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 2>), mgrid, dim3(128), a, stream);
-    default: return launch(reinterpret_cast<const void*>(&paged_decode_merge<T, LPH, 1>), mgrid, dim3(64), a, stream);
-  }
+  return launch_merge<T, LPH>(a, stream);
 }
 
 template <typename T, int LPH>
@@ -819,6 +825,24 @@ template <typename T>
 static hipError_t launch_generic(const DecodeArgs& a, hipStream_t stream) {
   return launch(reinterpret_cast<const void*>(&paged_decode_generic<T>),
                 dim3((unsigned)a.H, (unsigned)a.B), dim3(64), a, stream);
+}
+
+template <typename T>
+static hipError_t launch_merge_lph(const DecodeArgs& a, int lanes_per_head, hipStream_t stream) {
+  switch (lanes_per_head) {
+    case 4: return launch_merge<T, 4>(a, stream);
+    case 8: return launch_merge<T, 8>(a, stream);
+    case 16: return launch_merge<T, 16>(a, stream);
+    case 32: return launch_merge<T, 32>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_paged_merge(const DecodeArgs& a, int dtype, int lanes_per_head, hipStream_t stream) {
+  if (dtype == MGI_BF16) return launch_merge_lph<bf16_t>(a, lanes_per_head, stream);
+  if (dtype == MGI_F16) return launch_merge_lph<f16_t>(a, lanes_per_head, stream);
+  if (dtype == MGI_F32) return launch_merge_lph<float>(a, lanes_per_head, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_paged_decode(const DecodeArgs& a, int dtype, const DecodePlan& plan,

@@ -13,7 +13,10 @@
 // row-major, V transposed, two stages so one barrier per tile suffices).
 // Each wave computes S^T = K Q^T and O^T += V^T P^T with 16x16 MFMA tiles,
 // so a lane's accumulator column is one query row: the online-softmax state
-// (max, sum) is per lane and P needs no transpose.
+// (max, sum) is per lane and P needs no transpose. With split keys (a short
+// chunk after a long prefix), blockIdx.y selects a partition of the query
+// tile's keys and rows spanning several partitions write fp32 partials that
+// paged_decode_merge combines.
 //
 // Numerics: fp32 accumulation and softmax in the log2 domain; bf16 and f16
 // inputs use v_mfma_f32_16x16x32_bf16 / _f16 with P rounded to the input
@@ -177,10 +180,19 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   const int col = lane & 15, g = lane >> 4;
   const int qw0 = qt * QB + wave * 16 * QPW;
   const int kv_end = a.start + min(a.T, (qt + 1) * QB);
+  // Key partition (blockIdx.y) when the keys are split: this workgroup takes
+  // key tiles [tb, te) of its query tile's range and writes partials for the
+  // rows whose keys span several partitions.
+  const int part = (int)blockIdx.y;
+  const int ntiles_all = (kv_end + kTileKeys - 1) / kTileKeys;
+  const int tpp = a.part_keys > 0 ? a.part_keys / kTileKeys : ntiles_all;
+  const int tb = part * tpp;
+  if (tb >= ntiles_all) return;  // uniform: this query tile needs fewer partitions
+  const int key0 = tb * kTileKeys;
   const bool wave_active = qw0 < a.T;
   const int wave_first = a.start + qw0;
   const int wave_last = a.start + min(a.T, qw0 + 16 * QPW) - 1;
-  const int ntiles = (kv_end + kTileKeys - 1) / kTileKeys;
+  const int ntiles = min(ntiles_all, tb + tpp) - tb;  // this workgroup's tiles
 
   int qi[QPW], qpos[QPW];
 #pragma unroll
@@ -428,9 +440,9 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     // loads. Measured on MI355X: 16% faster than one tile ahead for a 512-row
     // chunk after a 512-token prefix, equal on 2048-row chunks.
     if (tid < kTileKeys) {
-      put_slots(0, key_rows(a, tid, kv_end));
-      put_slots(1, key_rows(a, kTileKeys + tid, kv_end));
-      slot_next = key_rows(a, 2 * kTileKeys + tid, kv_end);
+      put_slots(0, key_rows(a, key0 + tid, kv_end));
+      put_slots(1, key_rows(a, key0 + kTileKeys + tid, kv_end));
+      slot_next = key_rows(a, key0 + 2 * kTileKeys + tid, kv_end);
     }
     __syncthreads();
     load_tile(kr0, vr0, 0);
@@ -439,7 +451,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     __syncthreads();  // every wave has read tile 0's rows (stage 0)
     if (tid < kTileKeys) {
       put_slots(2, slot_next);
-      slot_next = key_rows(a, 3 * kTileKeys + tid, kv_end);
+      slot_next = key_rows(a, key0 + 3 * kTileKeys + tid, kv_end);
     }
     __syncthreads();
     if (ntiles > 2) load_tile(kr0, vr0, 0);  // tile 2 (rows stage 2 & 1 = 0)
@@ -447,12 +459,12 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     // One step: compute tile t, stage tile t+1 (held in set kn/vn) into LDS,
     // publish the rows of tile t+3, then load tile t+3 into the freed set.
     auto step = [&](int t, uint4 (&kn)[IPT][4], uint4 (&vn)[IPT][4]) {
-      const int kt0 = t * kTileKeys;
+      const int kt0 = key0 + t * kTileKeys;
       if (wave_active && kt0 <= wave_last) compute(t & 1, t & 3, kt0);
       if (t + 1 < ntiles) store_tile(kn, vn, (t + 1) & 1);
       if (tid < kTileKeys && t + 3 < ntiles) {
         put_slots(t + 3, slot_next);
-        slot_next = key_rows(a, (t + 4) * kTileKeys + tid, kv_end);
+        slot_next = key_rows(a, key0 + (t + 4) * kTileKeys + tid, kv_end);
       }
       __syncthreads();
       if (t + 3 < ntiles) load_tile(kn, vn, (t + 3) & 1);
@@ -466,26 +478,26 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     // in registers while tile t is computed; its block-table rows are in LDS
     // two tiles ahead.
     if (tid < kTileKeys) {
-      put_slots(0, key_rows(a, tid, kv_end));
-      if (ntiles > 1) slot_next = key_rows(a, kTileKeys + tid, kv_end);
+      put_slots(0, key_rows(a, key0 + tid, kv_end));
+      if (ntiles > 1) slot_next = key_rows(a, key0 + kTileKeys + tid, kv_end);
     }
     __syncthreads();
     load_tile(kr0, vr0, 0);
     if (tid < kTileKeys) {
       put_slots(1, slot_next);
-      if (ntiles > 2) slot_next = key_rows(a, 2 * kTileKeys + tid, kv_end);
+      if (ntiles > 2) slot_next = key_rows(a, key0 + 2 * kTileKeys + tid, kv_end);
     }
     store_tile(kr0, vr0, 0);
     __syncthreads();
     if (ntiles > 1) load_tile(kr0, vr0, 1);
 
     for (int t = 0; t < ntiles; ++t) {
-      const int kt0 = t * kTileKeys;
+      const int kt0 = key0 + t * kTileKeys;
       if (wave_active && kt0 <= wave_last) compute(t & 1, t & 3, kt0);
       if (t + 1 < ntiles) {
         if (tid < kTileKeys) {
           put_slots(t + 2, slot_next);
-          if (t + 3 < ntiles) slot_next = key_rows(a, (t + 3) * kTileKeys + tid, kv_end);
+          if (t + 3 < ntiles) slot_next = key_rows(a, key0 + (t + 3) * kTileKeys + tid, kv_end);
         }
         store_tile(kr0, vr0, (t + 1) & 1);
       }
@@ -494,11 +506,32 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     }
   }
 
-  // ---- normalise and store: lane holds out[qi, h, 16*db + 4*g + 0..3]
+  // ---- normalise and store: lane holds out[qi, h, 16*db + 4*g + 0..3]. With
+  // split keys, a row whose keys span several partitions writes its
+  // unnormalised state (max, sum, O) to slot (qi * H + h) * max_parts + part,
+  // the layout paged_decode_merge combines (a row at context start + qi + 1,
+  // partitions of part_keys keys); a row inside one partition is stored here.
 #pragma unroll
   for (int b = 0; b < QPW; ++b) {
     const float l = cross_group_sum(l_part[b]);
     if (qi[b] >= a.T) continue;
+    if (a.part_keys > 0) {
+      const int np = (a.start + qi[b] + a.part_keys) / a.part_keys;  // ceil((start + qi + 1) / part_keys)
+      if (part >= np) continue;  // the row's keys end before this partition
+      if (np > 1) {
+        const size_t slot = ((size_t)qi[b] * a.H + h) * a.max_parts + part;
+        if (g == 0) a.ws_ml[slot] = make_float2(m_run[b], l);
+        float* wa = a.ws_acc + slot * a.D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const int d0 = 16 * db + 4 * g;
+          if (d0 >= a.D) continue;
+          *reinterpret_cast<float4*>(wa + d0) =
+              make_float4(oacc[b][db][0], oacc[b][db][1], oacc[b][db][2], oacc[b][db][3]);
+        }
+        continue;
+      }
+    }
     const float inv = l > 0.f ? 1.f / l : 0.f;  // no visible valid key: zeros
     T* orow = reinterpret_cast<T*>(a.out) + (int64_t)qi[b] * a.o_st + (int64_t)h * a.o_sh;
 #pragma unroll
@@ -535,11 +568,15 @@ hipError_t launch_waves(const PrefillArgs& a, hipStream_t stream) {
   // 2048-row chunks by 8-19%. With one per CU (fp32 and the 256-wide bf16 /
   // f16 tiles fill the LDS) the grid runs in dynamic rounds, where the
   // longest-first order is better (the pairing cost fp32 16-33%).
+  // Split keys add a grid dimension of partitions (the pairing assumes one
+  // partition per query tile and is off then).
   PrefillArgs b = a;
-  b.pair_round = (per_cu == 2 && (a.H & 7) == 0 && a.cus % 8 == 0 && wgs > a.cus && wgs <= 2 * a.cus)
+  const bool split = a.part_keys > 0;
+  b.pair_round = (!split && per_cu == 2 && (a.H & 7) == 0 && a.cus % 8 == 0 && wgs > a.cus &&
+                  wgs <= 2 * a.cus)
                      ? a.cus / 8 : 0;
-  hipLaunchKernelGGL((paged_prefill_mfma<T, DP, WAVES, 1>), dim3((unsigned)wgs), dim3(64 * WAVES), 0,
-                     stream, b);
+  hipLaunchKernelGGL((paged_prefill_mfma<T, DP, WAVES, 1>),
+                     dim3((unsigned)wgs, split ? (unsigned)a.max_parts : 1u), dim3(64 * WAVES), 0, stream, b);
   return hipGetLastError();
 }
 

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "mgi_paged_decode_split_tokens",
     "mgi_paged_decode_balanced_waves",
     "mgi_paged_prefill",
+    "mgi_paged_prefill_workspace_bytes",
 )
 
 _lock = threading.Lock()
@@ -87,8 +88,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i64, _i64,                        # start_pos, T
         _i64, _i64, _i64, _i64, _i64, _i64,  # H D S N L layer
         ctypes.c_float,                    # scale
+        _p, ctypes.c_size_t,               # workspace, bytes
         _p,                                # stream
     ]
+    lib.mgi_paged_prefill_workspace_bytes.restype = ctypes.c_size_t
+    lib.mgi_paged_prefill_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _i]
 
 
 def lib() -> ctypes.CDLL:

@@ -194,6 +194,8 @@ def paged_prefill_hip(q: torch.Tensor, pool: KVBlockPool, block_table: torch.Ten
     out = torch.empty((t, h, d), dtype=q.dtype, device=q.device)
     if t == 0:
         return out
+    ws_bytes = int(lib.mgi_paged_prefill_workspace_bytes(int(start_pos), t, h, d, _native.DTYPE_CODES[q.dtype]))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     status = lib.mgi_paged_prefill(
         out.data_ptr(), _native.strides(out),
         q.data_ptr(), _native.strides(q),
@@ -203,6 +205,7 @@ def paged_prefill_hip(q: torch.Tensor, pool: KVBlockPool, block_table: torch.Ten
         block_table.shape[0], int(start_pos), t,
         h, d, S, N, L, int(layer_idx),
         1.0 / math.sqrt(d),
+        ws.data_ptr() if ws is not None else None, ws_bytes,
         _native.stream_handle(q.device),
     )
     _native.check(status)

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.lib()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mgi_abi_version() == 101
+    assert lib.mgi_abi_version() == 102
 
 
 def test_split_tokens_and_workspace_sizes():
@@ -96,7 +96,7 @@ def test_paged_prefill_rejects_bad_arguments_on_host():
         a.update(kw)
         return lib.mgi_paged_prefill(a["out"], st3, a["q"], st3, fake, fake, st5, st5, a["dtype"],
                                      a["bt"], 1, a["bt_it"], a["n_blocks"], a["start"], a["T"], a["H"],
-                                     a["D"], a["S"], a["N"], a["L"], a["layer"], a["scale"], None)
+                                     a["D"], a["S"], a["N"], a["L"], a["layer"], a["scale"], None, 0, None)
 
     assert call(T=0) == _native.MGI_OK  # nothing to do: no launch
     cases = [

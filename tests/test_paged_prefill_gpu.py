@@ -105,9 +105,57 @@ def test_matches_oracle(start, T, H, D, S, dtype):
     check(out, q, pool, table, start, layer)
 
 
+SPLIT_CASES = [
+    # start, T, H, D, S, keys per partition
+    (0, 406, 4, 128, 16, 64),
+    (1000, 200, 4, 128, 16, 192),
+    (511, 130, 2, 64, 16, 128),
+    (100, 20, 4, 256, 16, 64),
+    (64, 64, 8, 32, 16, 64),
+    (77, 150, 3, 128, 5, 128),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("start,T,H,D,S,keys", SPLIT_CASES)
+def test_forced_key_split_matches_oracle(monkeypatch, start, T, H, D, S, keys, dtype):
+    """Keys split into partitions of `keys` keys (partials merged by the
+    decode merge) against the oracle, with a NaN-filled workspace."""
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_SPLIT_KEYS", str(keys))
+    lib = hpd._native.lib()
+    code = hpd._native.DTYPE_CODES[dtype]
+    assert lib.mgi_paged_prefill_workspace_bytes(start, T, H, D, code) > 0
+    qkv, pool, table, layer = prefill_case(start, T, H, D, S, dtype, seed=13)
+    q = qkv.to(DEV)[:, 0]
+    torch.cuda.empty_cache()
+    torch.empty(1 << 24, device=DEV).fill_(float("nan"))  # freed: the workspace may reuse it
+    out = run_hip(q, pool, table, start, layer)
+    check(out, q, pool, table, start, layer)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_key_split_agrees_with_unsplit(monkeypatch, dtype):
+    """The automatic split (a small chunk after a long prefix) against the
+    same call with the split turned off: same softmax, summed in another
+    order."""
+    start, T, H, D, S = 3000, 256, 8, 128, 16
+    lib = hpd._native.lib()
+    assert lib.mgi_paged_prefill_workspace_bytes(start, T, H, D, hpd._native.DTYPE_CODES[dtype]) > 0
+    qkv, pool, table, layer = prefill_case(start, T, H, D, S, dtype, seed=17)
+    q = qkv.to(DEV)[:, 0]
+    split = run_hip(q, pool, table, start, layer)
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_SPLIT_KEYS", "-1")
+    assert lib.mgi_paged_prefill_workspace_bytes(start, T, H, D, hpd._native.DTYPE_CODES[dtype]) == 0
+    whole = run_hip(q, pool, table, start, layer)
+    check(split, q, pool, table, start, layer)
+    torch.testing.assert_close(split.float(), whole.float(), **TOL[dtype])
+
+
+@pytest.mark.parametrize("split_keys", ["0", "64"], ids=["auto", "split64"])
 @pytest.mark.parametrize("dtype", **DTYPES)
-def test_invalid_table_entries_are_masked(dtype):
+def test_invalid_table_entries_are_masked(monkeypatch, dtype, split_keys):
     """Entries outside [0, N) mask their block's keys; a row with no visible key is zero."""
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_SPLIT_KEYS", split_keys)
     qkv, pool, table, layer = prefill_case(40, 60, 4, 128, 16, dtype, seed=11)
     q = qkv.to(DEV)[:, 0]
     bad = table.clone()
