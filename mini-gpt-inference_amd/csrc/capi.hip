@@ -173,9 +173,15 @@ WorkspaceLayout workspace_layout(int64_t B, int64_t D, const SplitPlan& sp) {
 // Tokens loaded per pipeline stage of the fast kernel: 16 for bf16 and f16
 // and 8 for f32 (32 KiB of K+V per stage and wavefront at head_dim 128; two
 // stages in flight), or the largest S allows. Measured on MI355X this beats
-// smaller stages at higher occupancy. MINIVLLM_HIP_TOKENS_PER_STEP (8 or 16
+// smaller stages at higher occupancy on large calls. Small 2-byte calls,
+// whose table bound B*M*S*H*D*2 elements is at most kSmallCallKvBytes, take 8:
+// each wave's stream is short there and smaller stages end it with less
+// imbalance (B=64 x U[512, 4096], 4 heads: 62.3 -> 60.2 us; 8 heads: 112.3
+// -> 109.7 us; B=16 x 32 heads: 102.7 -> 100.4 us; 16 heads, a 2.1 GB bound:
+// 201.5 -> 206.8 us the other way). MINIVLLM_HIP_TOKENS_PER_STEP (8 or 16
 // for the 2-byte types, 4 or 8 for f32) overrides the choice when S allows it
 // (tuning).
+constexpr double kSmallCallKvBytes = 1.5e9;
 int tokens_per_step_override() {
   static const int v = [] {
     const char* e = std::getenv("MINIVLLM_HIP_TOKENS_PER_STEP");
@@ -344,7 +350,8 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
     int tok = 0;
     const int want = tokens_per_step_override();
     const bool two_byte = dtype != MGI_F32;
-    const int def = two_byte ? 16 : 8;
+    const double kv_bound = (double)B * (double)M * (double)S * (double)H * (double)D * (double)eb * 2.0;
+    const int def = two_byte ? (kv_bound <= kSmallCallKvBytes ? 8 : 16) : 8;
     for (int t : {want, def, 8, 4}) {
       if (t > 0 && ((two_byte && (t == 8 || t == 16)) || (!two_byte && (t == 4 || t == 8))) &&
           S % t == 0) {
