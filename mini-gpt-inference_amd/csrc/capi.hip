@@ -238,7 +238,10 @@ int64_t prefill_split_keys(int64_t start, int64_t T, int64_t H, int64_t D, int d
     total += tiles;
     longest = std::max(longest, tiles);
   }
-  if (forced > 0) return round_up(forced, 64) < longest * 64 ? round_up(forced, 64) : 0;
+  if (forced > 0) {
+    const int64_t pk = round_up(forced, 64);
+    return pk < longest * 64 && (start + T + pk - 1) / pk <= kMaxGridYZ ? pk : 0;  // partitions: grid y
+  }
   const int64_t slots = 2 * (int64_t)device_cus();
   if (nq * H >= slots) return 0;
   const int64_t k = std::max<int64_t>(2, (total * H + slots - 1) / slots);
@@ -246,7 +249,7 @@ int64_t prefill_split_keys(int64_t start, int64_t T, int64_t H, int64_t D, int d
   const double tile_us = 1.5 * (double)std::max<int64_t>(D, 64) / 128.0;
   const double partial_bytes = (double)split_partials(start, T, 64 * k) * (double)H * (double)(4 * D + 8);
   const double split_us = (double)k * tile_us + 8.0 + 2.0 * partial_bytes / 5.0e6;
-  return split_us < (double)longest * tile_us ? 64 * k : 0;
+  return split_us < (double)longest * tile_us && (start + T + 64 * k - 1) / (64 * k) <= kMaxGridYZ ? 64 * k : 0;
 }
 
 struct PrefillWorkspace {

@@ -52,6 +52,34 @@ def test_split_tokens_and_workspace_sizes():
     assert lib.mgi_paged_decode_split_tokens(1, 1, 128, 16, 256, 5000) == 2048
 
 
+def _prefill_ws(monkeypatch, split_keys, start, T, H, D, dtype=1):
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_SPLIT_KEYS", str(split_keys))
+    return _native.lib().mgi_paged_prefill_workspace_bytes(start, T, H, D, dtype)
+
+
+def test_prefill_split_workspace_sizes(monkeypatch):
+    """The key split's workspace: [T*H*parts*D f32, 256-aligned | T*H*parts
+    float2], parts = ceil((start + T) / keys per partition)."""
+    start, T, H, D, keys = 1000, 200, 4, 128, 192
+    parts = -(-(start + T) // keys)
+    n = T * H * parts
+    assert _prefill_ws(monkeypatch, keys, start, T, H, D) == ((n * D * 4 + 255) // 256) * 256 + n * 8
+    # forced sizes round up to whole 64-key tiles
+    assert _prefill_ws(monkeypatch, 130, start, T, H, D) == _prefill_ws(monkeypatch, 192, start, T, H, D)
+    # no split: turned off, fp32, a partition as long as the longest query tile,
+    # head dims the merge cannot take, more partitions than a grid dimension holds
+    assert _prefill_ws(monkeypatch, -1, start, T, H, D) == 0
+    assert _prefill_ws(monkeypatch, keys, start, T, H, D, dtype=0) == 0
+    assert _prefill_ws(monkeypatch, 1280, start, T, H, D) == 0
+    assert _prefill_ws(monkeypatch, keys, start, T, H, 20) == 0
+    assert _prefill_ws(monkeypatch, 64, 64 * 70000, 64, H, D) == 0
+    assert _prefill_ws(monkeypatch, 64, 64 * 60000, 64, H, D) > 0
+    # automatic: a short chunk after a long prefix splits, a first chunk does not
+    assert _prefill_ws(monkeypatch, 0, 3000, 256, 32, 128) > 0
+    assert _prefill_ws(monkeypatch, 0, 0, 512, 32, 128) == 0
+    assert _prefill_ws(monkeypatch, 0, 0, 4096, 32, 128) == 0
+
+
 def _i64(*xs):
     return (ctypes.c_int64 * len(xs))(*xs)
 
