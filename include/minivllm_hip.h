@@ -182,12 +182,16 @@ int64_t mgi_paged_decode_balanced_waves(int64_t B, int64_t H, int64_t D,
  * on the bf16 matrix cores with P rounded to bf16 for the PV product).
  * Layouts: q, out [T, H, D] (any strides); block_table [n_blocks] with
  * element stride bt_stride.
- * A chunk too small to fill the GPU (2-byte types) has its keys split over
- * several workgroups per query tile and the partials merged in a second
- * pass; workspace must then hold mgi_paged_prefill_workspace_bytes(...)
- * bytes for the same (start_pos, T, H, D, dtype). It may be NULL when that
- * is 0. Its contents need no initialisation; calls that overlap in time
- * need separate workspaces. (ABI 1.02 added workspace, workspace_bytes.)
+ * A short chunk after a long prefix (2-byte types, head_dim a multiple of
+ * 8, too few query tiles to fill the GPU, and a cost model that says it
+ * pays) has its keys split over several workgroups per query tile and the
+ * partials merged in a second pass; workspace must then hold
+ * mgi_paged_prefill_workspace_bytes(...) bytes for the same (start_pos, T,
+ * H, D, dtype), and it may be NULL when that is 0. Its contents need no
+ * initialisation; calls that overlap in time need separate workspaces.
+ * MINIVLLM_HIP_PREFILL_SPLIT_KEYS (read on every call, by both functions)
+ * turns the split off (-1) or forces that many keys per partition (> 0).
+ * (ABI 1.02 added workspace, workspace_bytes.)
  */
 int mgi_paged_prefill(void* out, const int64_t* out_strides, /* [3] */
                       const void* q, const int64_t* q_strides, /* [3] */
