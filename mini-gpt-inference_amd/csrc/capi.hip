@@ -220,8 +220,11 @@ int64_t split_partials(int64_t start, int64_t T, int64_t pk) {
 // plus its fp32 partials written and read back at ~5 TB/s. It pays after
 // long prefixes (a 256-row chunk after 3000 tokens, 32 heads: 80 -> 41 us)
 // and not for chunks whose causal triangle is most of the work (a 512-row
-// chunk at position 0: 18 -> 26 us split). 2-byte types with head_dim a
-// multiple of 8 only (the merge's lane layout).
+// chunk at position 0: 18 -> 26 us split), so it needs a prefix at least as
+// long as the chunk: the model alone would split a 1024-row first chunk of
+// 16 heads, measured 28.9 -> 34.1 us (two workgroups per CU slow each tile
+// and the diagonal tiles take the masking path). 2-byte types with head_dim
+// a multiple of 8 only (the merge's lane layout).
 // MINIVLLM_HIP_PREFILL_SPLIT_KEYS = -1 turns it off; > 0 forces that many
 // keys per partition, rounded up to 64, without the cost model (tuning and
 // tests; read on every call).
@@ -243,7 +246,7 @@ int64_t prefill_split_keys(int64_t start, int64_t T, int64_t H, int64_t D, int d
     return pk < longest * 64 && (start + T + pk - 1) / pk <= kMaxGridYZ ? pk : 0;  // partitions: grid y
   }
   const int64_t slots = 2 * (int64_t)device_cus();
-  if (nq * H >= slots) return 0;
+  if (nq * H >= slots || start < T) return 0;
   const int64_t k = std::max<int64_t>(2, (total * H + slots - 1) / slots);
   if (k >= longest) return 0;
   const double tile_us = 1.5 * (double)std::max<int64_t>(D, 64) / 128.0;

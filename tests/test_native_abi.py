@@ -77,7 +77,9 @@ def test_prefill_split_workspace_sizes(monkeypatch):
     # automatic: a short chunk after a long prefix splits, a first chunk does not
     assert _prefill_ws(monkeypatch, 0, 3000, 256, 32, 128) > 0
     assert _prefill_ws(monkeypatch, 0, 0, 512, 32, 128) == 0
+    assert _prefill_ws(monkeypatch, 0, 0, 1024, 16, 128) == 0
     assert _prefill_ws(monkeypatch, 0, 0, 4096, 32, 128) == 0
+    assert _prefill_ws(monkeypatch, 0, 512, 256, 16, 128) > 0
 
 
 def _i64(*xs):
