@@ -200,12 +200,15 @@ def _check_against_c_oracle(w, dtype, seqs=None):
         got = got[seqs]
     else:
         sub = w
-    want = c_oracle.paged_decode(*sub.compact_host(), threads=fx.oracle_threads())
+    args = list(sub.compact_host())
+    if dtype == torch.float16:  # exact in float32; the C oracle takes float32 or bfloat16 bits
+        args[:3] = [np.asarray(x, dtype=np.float32) for x in args[:3]]
+    want = c_oracle.paged_decode(*args, threads=fx.oracle_threads())
     np.testing.assert_allclose(got, want, **tol_for(dtype))
     return out
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 def test_decode_microbench_shape_matches_oracle(dtype):
     """B=64, H=32, D=128, S=16, ctx ~ U[512, 4096], 20k-block permuted pool."""
     print(f"  workload B=64 H=32 D=128 ctx U[512,4096] N=20000 {dtype}", flush=True)
