@@ -8,8 +8,8 @@ attention reads the pool (same stream). The decode backend is chosen by name:
   "reference"          PyTorch: index_put_ KV write + paged_attention_batch_online_v1
   "hip" / "triton_v0"  HIP kernels through libminivllm_hip.so: kv_append +
                        paged_attention_batch_hip ("triton_v0" is accepted so
-                       callers written for the reference's Triton backend run
-                       the HIP kernels unchanged)
+                       callers that select the reference's Triton backend by
+                       name run the HIP kernels)
 
 With a HIP backend, prefill KV writes go through the same kv_append kernel
 (one launch per chunk instead of a per-token copy loop). Both HIP entry

@@ -1,20 +1,42 @@
-"""Iteration scheduler (minivllm/scheduler.py:24-242).
+"""Per-iteration scheduling of decode tokens and prefill chunks.
 
-Each step plans, in order: one decode token for every RUNNING sequence,
-then prefill chunks for sequences already PREFILLING, then new admissions
-from the waiting queue -- bounded by ``max_num_batched_tokens``, the free
-KV blocks and ``max_running``. With ``preemption_policy="recompute"`` a
-shortage of blocks evicts unprotected active sequences (newest partial
-prefill first, then newest decode); an evicted sequence keeps its token
-history and is re-prefilled later. After any eviction in a step no new
-request is admitted in that step.
+Public surface of minivllm/scheduler.py (Scheduler, PrefillWorkItem,
+ScheduleOutput, the waiting / prefilling / running queues, preempt,
+retire_finished, num_preemptions). The decision order is what fixes the
+reference's block tables and known counts, so it is kept exactly:
+
+An iteration spends two budgets, batched tokens and free KV blocks, in three
+passes, each over a snapshot of its queue taken when the pass starts:
+
+1. decode: each RUNNING sequence, in queue order, asks for one token and
+   the blocks that token needs; the pass ends when fewer than one token is
+   left;
+2. continuing prefills: each PREFILLING sequence with prompt left asks for
+   a chunk; the pass ends when no token is left;
+3. admissions from the head of the waiting queue (FIFO), only if nothing was
+   evicted earlier in this iteration; it stops at the first request that
+   does not fit (max_running, the conservative reservation, the chunk or
+   its blocks).
+
+A chunk is min(prompt left, tokens left); under "recompute" it is further
+capped by what the sequence's blocks plus the free blocks can still hold.
+When a decode token, or (under "recompute") a prefill that could not get a
+single token, lacks blocks, victims are evicted until the blocks suffice or
+no candidate is left: newest PREFILLING first, then newest RUNNING, never
+the sequence asking, never one already planned this iteration, never one
+without blocks. A sequence that still does not fit is skipped for this
+iteration. Evicted sequences go back to the head of the waiting queue with
+their history (running ones keep prompt + generated[:-1] to rebuild).
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from collections.abc import Iterator
+from dataclasses import dataclass, field
 
 from .block_manager import BlockManager
 from .sequence import SequenceState, Status
+
+POLICIES = ("conservative", "recompute")
 
 
 @dataclass
@@ -35,171 +57,192 @@ class ScheduleOutput:
     num_scheduled_tokens: int
 
 
+@dataclass
+class _Budget:
+    """What is left to spend in one iteration, and what it has committed."""
+    tokens: int
+    blocks: int
+    planned: set[int] = field(default_factory=set)   # id() of sequences planned this iteration
+    evicted: bool = False
+
+    def commit(self, seq: SequenceState, tokens: int, blocks: int) -> None:
+        self.tokens -= tokens
+        self.blocks -= blocks
+        self.planned.add(id(seq))
+
+
 class Scheduler:
     def __init__(self, block_manager: BlockManager, max_running: int, max_num_batched_tokens: int,
                  preemption_policy: str = "conservative"):
-        if preemption_policy not in ("conservative", "recompute"):
+        if preemption_policy not in POLICIES:
             raise ValueError("preemption_policy must be 'conservative' or 'recompute'")
-        self.waiting: list[SequenceState] = []
-        self.prefilling: list[SequenceState] = []
-        self.running: list[SequenceState] = []
         self.block_manager = block_manager
         self.max_running = max_running
         self.max_num_batched_tokens = max_num_batched_tokens
         self.preemption_policy = preemption_policy
+        self.waiting: list[SequenceState] = []
+        self.prefilling: list[SequenceState] = []
+        self.running: list[SequenceState] = []
         self.num_preemptions = 0
 
-    # ---------------------------------------------------------- capacity
+    # ------------------------------------------------------------ accounting
 
-    def _max_kv_blocks(self, seq: SequenceState) -> int:
-        # The final sampled token never enters the KV pool.
+    @property
+    def _recompute(self) -> bool:
+        return self.preemption_policy == "recompute"
+
+    def _lifetime_blocks(self, seq: SequenceState) -> int:
+        """Blocks a request holds at its longest: every token but the last
+        sampled one enters the pool."""
         S = self.block_manager.block_size
-        return (seq.max_tokens - 1 + S - 1) // S
+        return -(-(seq.max_tokens - 1) // S)
 
-    def _can_admit_without_preemption(self, seq: SequenceState) -> bool:
-        committed = sum(self._max_kv_blocks(s) for s in self.running + self.prefilling)
-        return committed + self._max_kv_blocks(seq) <= self.block_manager.num_blocks
+    def _reservation_fits(self, seq: SequenceState) -> bool:
+        """Conservative admission: the lifetime blocks of every active request
+        plus this one fit the pool."""
+        held = sum(self._lifetime_blocks(s) for s in (*self.running, *self.prefilling))
+        return held + self._lifetime_blocks(seq) <= self.block_manager.num_blocks
+
+    def _chunk(self, seq: SequenceState, budget: _Budget) -> int:
+        """Prefill tokens to plan for `seq` now (0: none fit)."""
+        n = min(seq.remaining_prompt_tokens, budget.tokens)
+        if self._recompute:
+            S = self.block_manager.block_size
+            room = (len(seq.block_table) + budget.blocks) * S - seq.length
+            n = min(n, max(room, 0))
+        return n
+
+    # -------------------------------------------------------------- requests
 
     def add_request(self, seq: SequenceState) -> None:
         if not seq.prompt_tokens or seq.max_tokens <= seq.prompt_length:
-            raise ValueError("prompt must be nonempty and output token must be positive")
-        if self._max_kv_blocks(seq) > self.block_manager.num_blocks:
-            raise ValueError("request's maximum KV demand exceeds total block capacity")
+            raise ValueError("a request needs a nonempty prompt and at least one output token")
+        if self._lifetime_blocks(seq) > self.block_manager.num_blocks:
+            raise ValueError("the request's largest KV footprint exceeds the block pool")
         self.waiting.append(seq)
 
-    # ----------------------------------------------------------- eviction
-
     def preempt(self, seq: SequenceState) -> None:
-        """Evicts an active sequence's KV and requeues it first. Between steps only."""
+        """Releases an active request's KV and puts it first in the waiting
+        queue. Only between iterations."""
         if seq in self.running:
-            assert seq.generated_tokens, "RUNNING request has no output token"
-            assert seq.last_token == seq.generated_tokens[-1]
-            seq.recompute_tokens = seq.prompt_tokens + seq.generated_tokens[:-1]
-            assert len(seq.recompute_tokens) == seq.length
+            if not seq.generated_tokens or seq.last_token != seq.generated_tokens[-1]:
+                raise RuntimeError(f"{seq.seq_id}: running request without a pending output token")
+            # Rebuild everything whose KV was committed; the pending token
+            # stays the next decode input.
+            rebuild = seq.prompt_tokens + seq.generated_tokens[:-1]
+            if len(rebuild) != seq.length:
+                raise RuntimeError(f"{seq.seq_id}: committed KV does not match its token history")
+            seq.recompute_tokens = rebuild
             self.running.remove(seq)
         elif seq in self.prefilling:
-            # Partial prefill KV is discarded; an interrupted recompute keeps
-            # its recompute_tokens, an ordinary prefill keeps None.
+            # The partial KV is dropped; recompute_tokens (if any) stay.
             self.prefilling.remove(seq)
         else:
-            raise ValueError("Only active requests may be preempted")
-        self.num_preemptions += 1
-        seq.num_preemptions += 1
-        self.block_manager.free(seq)
+            raise ValueError(f"{seq.seq_id} is not active and cannot be preempted")
+        self.block_manager.free(seq)     # also clears the table and length
         seq.prompt_pos = 0
         seq.status = Status.WAITING
+        seq.num_preemptions += 1
+        self.num_preemptions += 1
         self.waiting.insert(0, seq)
 
     def retire_finished(self) -> None:
-        alive = []
+        still = []
         for seq in self.running:
-            if seq.is_finished():
-                seq.status = Status.FINISHED
-                self.block_manager.free(seq)
-            else:
-                alive.append(seq)
-        self.running = alive
-
-    def _choose_victim(self, target: SequenceState, protected_ids: set[int]) -> SequenceState | None:
-        for seq in [*reversed(self.prefilling), *reversed(self.running)]:
-            if seq is target or id(seq) in protected_ids:
+            if not seq.is_finished():
+                still.append(seq)
                 continue
-            if seq.block_table:
-                return seq
-        return None
+            seq.status = Status.FINISHED
+            self.block_manager.free(seq)
+        self.running = still
 
-    def _free_for(self, target: SequenceState, needed: int, available: int,
-                  protected_ids: set[int]) -> tuple[int, bool]:
-        """Evicts victims until `needed` blocks are available (recompute policy)."""
-        evicted = False
-        if self.preemption_policy != "recompute":
-            return available, evicted
-        while available < needed:
-            victim = self._choose_victim(target, protected_ids)
-            if victim is None:
-                break
-            released = len(victim.block_table)
+    # -------------------------------------------------------------- eviction
+
+    def _victims(self, asking: SequenceState, budget: _Budget) -> Iterator[SequenceState]:
+        """Eviction candidates in order: newest prefill first, then newest decode."""
+        for seq in (*reversed(self.prefilling), *reversed(self.running)):
+            if seq is not asking and id(seq) not in budget.planned and seq.block_table:
+                yield seq
+
+    def _make_room(self, asking: SequenceState, blocks: int, budget: _Budget) -> bool:
+        """Evicts (recompute policy only) until `blocks` free blocks are
+        available to `asking`; True when they are."""
+        if budget.blocks >= blocks:
+            return True
+        if not self._recompute:
+            return False
+        for victim in self._victims(asking, budget):
+            budget.blocks += len(victim.block_table)
             self.preempt(victim)
-            available += released
-            evicted = True
-        return available, evicted
+            budget.evicted = True
+            if budget.blocks >= blocks:
+                return True
+        return False
 
-    def _prefill_chunk_size(self, seq: SequenceState, remaining_budget: int, available_blocks: int) -> int:
-        desired = min(seq.remaining_prompt_tokens, remaining_budget)
-        if self.preemption_policy != "recompute":
-            return desired
-        # Only what already-held plus uncommitted blocks can store.
-        fit = (len(seq.block_table) + available_blocks) * self.block_manager.block_size - seq.length
-        return min(desired, max(0, fit))
+    # ---------------------------------------------------------------- passes
 
-    # ----------------------------------------------------------- planning
-
-    def schedule(self) -> ScheduleOutput:
-        prefill: list[PrefillWorkItem] = []
-        decode: list[SequenceState] = []
-        budget = self.max_num_batched_tokens
-        free_blocks = len(self.block_manager.free_blocks)
-        protected: set[int] = set()      # planned this step: never evicted
-        evicted_this_step = False
-
+    def _plan_decodes(self, budget: _Budget) -> list[SequenceState]:
+        out = []
         for seq in list(self.running):
-            if budget < 1:
+            if budget.tokens < 1:
                 break
-            if seq.status != Status.RUNNING:
-                continue                 # evicted earlier in this step
-            needed = self.block_manager.num_new_blocks_needed(seq, 1)
-            if needed > free_blocks:
-                free_blocks, did = self._free_for(seq, needed, free_blocks, protected)
-                evicted_this_step |= did
-            if needed > free_blocks:
+            if seq.status is not Status.RUNNING:       # evicted earlier in this pass
                 continue
-            decode.append(seq)
-            protected.add(id(seq))
-            budget -= 1
-            free_blocks -= needed
+            need = self.block_manager.num_new_blocks_needed(seq, 1)
+            if not self._make_room(seq, need, budget):
+                continue
+            budget.commit(seq, 1, need)
+            out.append(seq)
+        return out
 
+    def _plan_prefills(self, budget: _Budget) -> list[PrefillWorkItem]:
+        out = []
         for seq in list(self.prefilling):
-            if budget <= 0:
+            if budget.tokens <= 0:
                 break
-            if seq.status != Status.PREFILLING:
+            if seq.status is not Status.PREFILLING or seq.remaining_prompt_tokens <= 0:
                 continue
-            if seq.remaining_prompt_tokens <= 0:
+            n = self._chunk(seq, budget)
+            if n == 0 and self._recompute:
+                self._make_room(seq, 1, budget)
+                n = self._chunk(seq, budget)
+            if n <= 0:
                 continue
-            chunk = self._prefill_chunk_size(seq, budget, free_blocks)
-            if chunk == 0 and self.preemption_policy == "recompute":
-                free_blocks, did = self._free_for(seq, 1, free_blocks, protected)
-                evicted_this_step |= did
-                chunk = self._prefill_chunk_size(seq, budget, free_blocks)
-            if chunk <= 0:
+            need = self.block_manager.num_new_blocks_needed(seq, n)
+            if need > budget.blocks:
                 continue
-            needed = self.block_manager.num_new_blocks_needed(seq, chunk)
-            if needed > free_blocks:
-                continue
-            prefill.append(PrefillWorkItem(seq, seq.prompt_pos, chunk))
-            protected.add(id(seq))
-            budget -= chunk
-            free_blocks -= needed
+            budget.commit(seq, n, need)
+            out.append(PrefillWorkItem(seq, seq.prompt_pos, n))
+        return out
 
-        # After an eviction, admit nobody this step (avoids evict/re-admit ping-pong).
-        while self.waiting and budget > 0 and not evicted_this_step:
+    def _plan_admissions(self, budget: _Budget) -> list[PrefillWorkItem]:
+        out = []
+        while self.waiting and budget.tokens > 0:
             if len(self.running) + len(self.prefilling) >= self.max_running:
                 break
             seq = self.waiting[0]
-            if self.preemption_policy == "conservative" and not self._can_admit_without_preemption(seq):
+            if not self._recompute and not self._reservation_fits(seq):
                 break
-            chunk = self._prefill_chunk_size(seq, budget, free_blocks)
-            if chunk <= 0:
+            n = self._chunk(seq, budget)
+            if n <= 0:
                 break
-            needed = self.block_manager.num_new_blocks_needed(seq, chunk)
-            if needed > free_blocks:
+            need = self.block_manager.num_new_blocks_needed(seq, n)
+            if need > budget.blocks:
                 break
             self.waiting.pop(0)
             seq.status = Status.PREFILLING
             self.prefilling.append(seq)
-            prefill.append(PrefillWorkItem(seq, seq.prompt_pos, chunk))
-            protected.add(id(seq))
-            budget -= chunk
-            free_blocks -= needed
+            budget.commit(seq, n, need)
+            out.append(PrefillWorkItem(seq, seq.prompt_pos, n))
+        return out
 
+    def schedule(self) -> ScheduleOutput:
+        budget = _Budget(tokens=self.max_num_batched_tokens, blocks=len(self.block_manager.free_blocks))
+        decode = self._plan_decodes(budget)
+        prefill = self._plan_prefills(budget)
+        # An eviction closes admissions for this iteration: the evicted
+        # request would otherwise take its blocks straight back.
+        if not budget.evicted:
+            prefill += self._plan_admissions(budget)
         return ScheduleOutput(prefill=prefill, decode=decode,
-                              num_scheduled_tokens=self.max_num_batched_tokens - budget)
+                              num_scheduled_tokens=self.max_num_batched_tokens - budget.tokens)

@@ -207,3 +207,226 @@ def run_c1(case: dict, device, backend: str, prefill_mode: str | None = None):
             manager.check_invariants([s for s in seqs if s.status != Status.FINISHED])
     assert all(s.status == Status.FINISHED for s in seqs)
     return [s.generated_tokens for s in seqs], rt
+
+
+# ------------------------------------------------------ lock-step comparison
+
+class _Probe:
+    """Wraps one runtime so each step records its schedule, its decode logits
+    and, per sequence, the end of the KV its current prefill wrote."""
+
+    def __init__(self, rt: MiniRuntime, seqs):
+        self.rt, self.seqs = rt, seqs
+        self.by_id = {s.seq_id: s for s in seqs}
+        self.plan = None
+        self.logits = None
+        self.decoded: list[str] = []
+        self.prefill_end: dict[str, int] = {}
+        schedule, decode, prefill = rt.scheduler.schedule, rt.runner.decode_batch, rt.runner.prefill_chunk
+
+        def schedule_probe():
+            out = schedule()
+            self.plan = ([(i.seq.seq_id, i.start_pos, i.num_tokens) for i in out.prefill],
+                         [s.seq_id for s in out.decode])
+            return out
+
+        def decode_probe(sequences):
+            logits, tokens = decode(sequences)
+            self.logits = logits.float()
+            self.decoded = [s.seq_id for s in sequences]
+            return logits, tokens
+
+        def prefill_probe(seq, start_pos, num_tokens):
+            out = prefill(seq=seq, start_pos=start_pos, num_tokens=num_tokens)
+            # Chunks of one incarnation are contiguous from position 0.
+            self.prefill_end[seq.seq_id] = start_pos + num_tokens
+            return out
+
+        rt.scheduler.schedule = schedule_probe
+        rt.runner.decode_batch = decode_probe
+        rt.runner.prefill_chunk = prefill_probe
+
+    def step(self) -> None:
+        self.plan, self.logits, self.decoded = None, None, []
+        self.rt.step()
+
+
+def _token_slots(seq: SequenceState, S: int) -> list[int]:
+    t = seq.block_table
+    return [t[p // S] * S + p % S for p in range(seq.length)]
+
+
+class Lockstep:
+    """The reference runtime and the HIP runtime stepped alternately over one
+    model, one request set and two KV pools of the same size, as
+    experiments/gpu_day6_runtime_decode_ab.py:59-130 steps its two backends.
+    Prefill uses the model's prefill mode in both, so the only difference
+    between the runs is the decode attention backend ("reference" = the
+    PyTorch online-softmax path, "hip" = kv_append + the HIP decode kernel).
+
+    ``step()`` advances both runtimes by one iteration and checks:
+      * identical schedules (prefill chunks, decode batch order), sequence
+        states (status, length, prompt position, block table) and lifecycle
+        counts -- the schedule is token-independent, so this holds even
+        after a token stream diverges;
+      * decode logits of every row whose inputs still agree within
+        ``logit_tol`` (|hip - ref| <= atol + rtol * |ref|);
+      * greedy tokens identical, except that a stream may diverge where the
+        reference's top-2 logit margin is below ``tie_margin``; the diverged
+        sequence is left out of the logit and KV checks from then on (its
+        inputs differ);
+      * logical KV of every active, not diverged sequence read through its
+        block table: bit-identical in layer 0 (its input is the token and
+        position embedding alone) and at every position the current prefill
+        wrote (prefill is shared and deterministic), within ``kv_tol`` at
+        positions decode wrote in later layers (the decode attention outputs
+        differ in rounding). ``kv_tol=None`` checks through
+        KVBlockPool.gather_sequence on the host instead, with ``kv_tol``
+        replaced by ``logit_tol`` everywhere, as the reference harness does.
+
+    Statistics of every check accumulate in ``stats``.
+    """
+
+    def __init__(self, spec: RuntimeSpec, model: MiniGPT, prompts, device, dtype, *,
+                 logit_tol: tuple[float, float], tie_margin: float, kv_tol: tuple[float, float] | None):
+        self.model = model
+        self.logit_tol, self.tie_margin, self.kv_tol = logit_tol, tie_margin, kv_tol
+        self.ref = _Probe(*make_runtime(spec, model, prompts, device, dtype))
+        self.hip = _Probe(*make_runtime(spec, model, prompts, device, dtype))
+        self.diverged: dict[str, tuple[int, int, float]] = {}   # seq_id -> (step, token index, margin)
+        self.stats = {"steps": 0, "decode_rows_checked": 0, "max_logit_abs": 0.0, "max_logit_excess": 0.0,
+                      "kv_tokens_checked": 0, "kv_exact_tokens": 0, "max_kv_abs": 0.0, "max_kv_excess": 0.0,
+                      "preemptions": 0, "recomputed_seqs": set()}
+
+    @property
+    def finished(self) -> bool:
+        return all(s.status == Status.FINISHED for s in self.ref.seqs)
+
+    def step(self) -> None:
+        step = self.stats["steps"] + 1
+        for backend, probe in (("reference", self.ref), ("hip", self.hip)):
+            self.model.set_decode_attention_backend(backend)
+            probe.step()
+        self.stats["steps"] = step
+        a, b = self.ref, self.hip
+        if a.plan != b.plan:
+            raise AssertionError(f"step {step}: schedules differ: {a.plan} vs {b.plan}")
+        if a.decoded != b.decoded:
+            raise AssertionError(f"step {step}: decode batches differ")
+        sa, sb = a.rt.metrics_summary(), b.rt.metrics_summary()
+        for key in ("iterations", "scheduled_tokens", "prefill_tokens", "decode_tokens", "output_tokens",
+                    "preemptions", "repeated_kv_tokens"):
+            if sa[key] != sb[key]:
+                raise AssertionError(f"step {step}: {key} {sa[key]} vs {sb[key]}")
+        self.stats["preemptions"] = sa["preemptions"]
+        for sid, _, _ in a.plan[0]:
+            if a.by_id[sid].num_preemptions:
+                self.stats["recomputed_seqs"].add(sid)
+        self._check_states(step)
+        self._check_decode(step)
+        self._check_kv(step)
+
+    def _check_states(self, step: int) -> None:
+        for x in self.ref.seqs:
+            y = self.hip.by_id[x.seq_id]
+            if (x.status, x.length, x.prompt_pos, x.block_table, x.num_preemptions) != \
+                    (y.status, y.length, y.prompt_pos, y.block_table, y.num_preemptions):
+                raise AssertionError(f"step {step}: state of {x.seq_id} differs")
+            if len(x.generated_tokens) != len(y.generated_tokens):
+                raise AssertionError(f"step {step}: {x.seq_id} generated counts differ")
+
+    def _check_decode(self, step: int) -> None:
+        a, b = self.ref, self.hip
+        if (a.logits is None) != (b.logits is None):
+            raise AssertionError(f"step {step}: decode ran in one runtime only")
+        atol, rtol = self.logit_tol
+        if a.logits is not None:
+            keep = [i for i, sid in enumerate(a.decoded) if sid not in self.diverged]
+            if keep:
+                rows = torch.tensor(keep, device=a.logits.device)
+                ra, rb = a.logits.index_select(0, rows), b.logits.index_select(0, rows)
+                diff = (ra - rb).abs()
+                excess = (diff - (atol + rtol * ra.abs())).max().item()
+                self.stats["max_logit_abs"] = max(self.stats["max_logit_abs"], diff.max().item())
+                self.stats["max_logit_excess"] = max(self.stats["max_logit_excess"], excess)
+                self.stats["decode_rows_checked"] += len(keep)
+                if excess > 0:
+                    raise AssertionError(f"step {step}: decode logits differ by {diff.max().item():.4g} "
+                                         f"(tolerance atol {atol} + rtol {rtol} * |ref|)")
+        # Tokens: every stream not yet diverged must agree; a new divergence
+        # is allowed only at a near tie of the reference's logits.
+        for x in a.seqs:
+            if x.seq_id in self.diverged:
+                continue
+            y = b.by_id[x.seq_id]
+            if x.generated_tokens == y.generated_tokens:
+                continue
+            k = next(i for i, (p, q) in enumerate(zip(x.generated_tokens, y.generated_tokens)) if p != q)
+            if k != len(x.generated_tokens) - 1 or a.logits is None or x.seq_id not in a.decoded:
+                raise AssertionError(f"step {step}: {x.seq_id} token {k} differs outside a decode step")
+            row = a.logits[a.decoded.index(x.seq_id)]
+            top = torch.topk(row, 2).values.tolist()
+            margin = top[0] - top[1]
+            if margin >= self.tie_margin:
+                raise AssertionError(f"step {step}: {x.seq_id} token {k} differs at reference top-2 "
+                                     f"margin {margin:.4g} (allowed only below {self.tie_margin})")
+            self.diverged[x.seq_id] = (step, k, margin)
+
+    def _check_kv(self, step: int) -> None:
+        live = [x for x in self.ref.seqs
+                if x.status != Status.FINISHED and x.length > 0 and x.seq_id not in self.diverged]
+        if not live:
+            return
+        if self.kv_tol is None:
+            atol, rtol = self.logit_tol
+            for x in live:
+                y = self.hip.by_id[x.seq_id]
+                ka, va = self.ref.rt.runner.kv_pool.gather_sequence(x)
+                kb, vb = self.hip.rt.runner.kv_pool.gather_sequence(y)
+                for u, w in ((ka, kb), (va, vb)):
+                    torch.testing.assert_close(w, u, atol=atol, rtol=rtol,
+                                               msg=lambda m: f"step {step}: logical KV of {x.seq_id}: {m}")
+                    self.stats["max_kv_abs"] = max(self.stats["max_kv_abs"], (u - w).abs().max().item())
+                self.stats["kv_tokens_checked"] += x.length
+            return
+        pa, pb = self.ref.rt.runner.kv_pool, self.hip.rt.runner.kv_pool
+        S, dev = pa.block_size, pa.k.device
+        slots, exact = [], []
+        for x in live:
+            slots += _token_slots(x, S)
+            end = self.ref.prefill_end.get(x.seq_id, 0)
+            exact += [p < end for p in range(x.length)]
+        idx = torch.tensor(slots, dtype=torch.long, device=dev)
+        ex = torch.tensor(exact, dtype=torch.bool, device=dev)
+        atol, rtol = self.kv_tol
+        L, N, _, H, D = pa.k.shape
+        for layer in range(L):
+            for ta, tb in ((pa.k, pb.k), (pa.v, pb.v)):
+                u = ta[layer].reshape(N * S, H, D).index_select(0, idx)
+                w = tb[layer].reshape(N * S, H, D).index_select(0, idx)
+                same = (u.view(torch.int16) == w.view(torch.int16)).all(dim=(1, 2)) \
+                    if u.element_size() == 2 else (u.view(torch.int32) == w.view(torch.int32)).all(dim=(1, 2))
+                must = ex if layer > 0 else torch.ones_like(ex)
+                bad = must & ~same
+                if bool(bad.any()):
+                    raise AssertionError(f"step {step}: layer {layer} KV not bit-identical at "
+                                         f"{int(bad.sum())} prefill-written or layer-0 positions")
+                uf, wf = u.float(), w.float()
+                diff = (uf - wf).abs()
+                excess = (diff - (atol + rtol * uf.abs())).amax(dim=(1, 2))
+                worst = excess.max().item()
+                self.stats["max_kv_abs"] = max(self.stats["max_kv_abs"], diff.max().item())
+                self.stats["max_kv_excess"] = max(self.stats["max_kv_excess"], worst)
+                if worst > 0:
+                    raise AssertionError(f"step {step}: layer {layer} logical KV differs by "
+                                         f"{diff.max().item():.4g} (tolerance atol {atol} + rtol {rtol} * |ref|)")
+        self.stats["kv_tokens_checked"] += len(slots)
+        self.stats["kv_exact_tokens"] += int(ex.sum())
+
+    def finish_checks(self) -> None:
+        """End-of-run checks of a completed workload (no KV leak, invariants)."""
+        for probe in (self.ref, self.hip):
+            bm = probe.rt.block_manager
+            if bm.block_owner or len(bm.free_blocks) != bm.num_blocks:
+                raise AssertionError("KV capacity leak after the completed workload")
+            bm.check_invariants(probe.seqs)

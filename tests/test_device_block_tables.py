@@ -1,4 +1,5 @@
-"""Device-resident block tables (minivllm.device_block_tables) on the CPU.
+"""Device-resident block tables (minivllm.device_block_tables), on the CPU
+and (the churn test, marked gpu) on the GPU the runtime keeps them on.
 
 Each step's gather must equal the -1 padded tables the reference builds on the
 host (minivllm/model_runner.py:176-201), through appends, preemption rewrites
@@ -23,17 +24,18 @@ def padded(tables, M):
 def run_step(dt, ids, tables):
     rows, upd = dt.stage(ids, tables)
     B = len(ids)
-    step = pack_decode_step([0] * B, [1] * B, [0] * B, rows, upd, B)
+    step = pack_decode_step([0] * B, [1] * B, [0] * B, rows, upd, B).to(dt.table.device)
     dt.apply(step[5 * B:])
     M = max(len(t) for t in tables)
     _, meta = step_metadata(step, B, dt, M)
     return meta.block_tables, len(upd) // 3
 
 
+@pytest.mark.parametrize("device", ["cpu", pytest.param("cuda", marks=pytest.mark.gpu)])
 @pytest.mark.parametrize("seed", range(4))
-def test_random_churn_matches_host_tables(seed):
+def test_random_churn_matches_host_tables(seed, device):
     rng = random.Random(seed)
-    dt = DeviceBlockTables("cpu", rows=3, cols=2)
+    dt = DeviceBlockTables(device, rows=3, cols=2)
     live: dict[str, list[int]] = {}
     events = {"append": 0, "shrink": 0, "rewrite": 0, "evict": 0, "grow_rows": 0, "grow_cols": 0}
     next_id = 0
