@@ -373,6 +373,10 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
     }
   }
 
+  // Partition mode launches one grid row per partition.
+  if (plan.path == DecodePath::kFast && sp.bal_waves == 0 && sp.max_parts > kMaxGridYZ)
+    return fail(MGI_EUNSUPPORTED, "more than 65535 partitions per context (split_tokens too small for the table)");
+
   DecodeArgs a{};
   a.out = out;
   a.o_sb = out_strides[0];

@@ -13,12 +13,16 @@ records inputs and outputs as a small fixture:
 Prompts come from torch.Generator seeded 10_000 + 100 * B + P.
 
 Usage (build container only):  python tests/golden/make_c1_greedy_tokens.py
+The reference modules are compiled from their .py sources into a temporary
+bytecode cache (sys.pycache_prefix); the .pyc files shipped in the reference
+tree are never read.
 """
 from __future__ import annotations
 
 import json
 import math
 import sys
+import tempfile
 from pathlib import Path
 
 REFERENCE = "/root/reference"
@@ -76,6 +80,10 @@ def run_case(B: int, P: int) -> dict:
 
 
 def main() -> None:
+    # Compile the reference's .py sources into a fresh bytecode cache, so no
+    # .pyc shipped next to them is ever loaded.
+    sys.pycache_prefix = tempfile.mkdtemp(prefix="ref_pycache_")
+    sys.dont_write_bytecode = False
     sys.path.insert(0, REFERENCE)
     import torch
 

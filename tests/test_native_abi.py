@@ -115,6 +115,26 @@ def test_paged_decode_rejects_bad_arguments_on_host():
         assert msg in lib.mgi_last_error().decode(), (kw, lib.mgi_last_error())
 
 
+def test_paged_decode_rejects_too_many_partitions_on_host():
+    """A small split_tokens over a wide table would need more partitions than a
+    grid dimension holds: refused before any launch (the pointers are never
+    dereferenced)."""
+    lib = _native.lib()
+    B, H, D, S, N, M = 1, 1, 128, 16, 8, 70000
+    pool = _i64(N * S * H * D, S * H * D, H * D, D, 1)
+    st3, st2 = _i64(H * D, D, 1), _i64(M, 1)
+    fake = 0x10000
+
+    def call(split):
+        return lib.mgi_paged_decode(fake, st3, fake, st3, fake, fake, pool, pool, _native.MGI_BF16,
+                                    fake, st2, 1, fake, 1, 1, B, H, D, S, N, M, 1, 0, 0.1, split,
+                                    fake, 1 << 40, None)
+
+    assert call(S) == _native.MGI_EUNSUPPORTED
+    assert "65535 partitions" in lib.mgi_last_error().decode()
+    assert lib.mgi_paged_decode_split_tokens(B, H, D, S, M, S) == S   # 70000 partitions of S tokens
+
+
 def test_paged_prefill_rejects_bad_arguments_on_host():
     lib = _native.lib()
     st3, st5 = _i64(1, 1, 1), _i64(1, 1, 1, 1, 1)
