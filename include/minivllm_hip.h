@@ -60,7 +60,7 @@ const char* mgi_last_error(void);
 /* ABI version of this library (major*100 + minor). 1.01 added
  * mgi_paged_decode_balanced_waves and the even split of split_tokens = 0;
  * 1.02 the prefill key split (mgi_paged_prefill's workspace arguments and
- * mgi_paged_prefill_workspace_bytes). */
+ * mgi_paged_prefill_workspace_bytes); 1.03 mgi_paged_decode_noalloc. */
 int mgi_abi_version(void);
 
 /*
@@ -143,6 +143,36 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, /* [3] */
                      float scale, int64_t split_tokens,
                      void* workspace, size_t workspace_bytes,
                      void* stream);
+
+/*
+ * mgi_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Same arguments (minus workspace and workspace_bytes), checks, kernels and
+ * results as mgi_paged_decode; the split workspace is a 32 MiB array the
+ * library holds on every device it runs on, for the life of the process
+ * (resolved on the first call per device; nothing is allocated, here or
+ * later). A call whose split needs more than that
+ * (mgi_paged_decode_workspace_bytes > 32 MiB; the automatic split needs
+ * about 13 MiB at head_dim 128 whatever B and the context lengths, explicit
+ * small partitions over many long contexts can need more) returns
+ * MGI_EUNSUPPORTED without launching. All calls on one device share the
+ * array: calls that overlap in time on one device (other streams, or graph
+ * replays beside eager calls) race and give wrong results. Added in ABI 1.03.
+ */
+int mgi_paged_decode_noalloc(void* out, const int64_t* out_strides, /* [3] */
+                             const void* q, const int64_t* q_strides, /* [3] */
+                             const void* k_pool, const void* v_pool,
+                             const int64_t* k_pool_strides, /* [5] */
+                             const int64_t* v_pool_strides, /* [5] */
+                             int dtype,
+                             const void* block_tables, const int64_t* bt_strides, /* [2] */
+                             int bt_itype,
+                             const void* context_lens, int64_t cl_stride, int cl_itype,
+                             int64_t B, int64_t H, int64_t D, int64_t S, int64_t N,
+                             int64_t M, int64_t L, int64_t layer_idx,
+                             float scale, int64_t split_tokens,
+                             void* stream);
 
 /* Workspace bytes mgi_paged_decode needs for these sizes (0 if none). */
 size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D,

@@ -7,6 +7,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "mgi_internal.h"
@@ -272,13 +273,54 @@ PrefillWorkspace prefill_workspace(int64_t start, int64_t T, int64_t H, int64_t 
   return w;
 }
 
+// Scratch of mgi_paged_decode_noalloc: the split workspace of callers that
+// cannot allocate. One copy per device, resident for the life of the process.
+// In host code `scratch` names a host-side stand-in; its device address comes
+// from hipGetSymbolAddress, per device (each holds its own copy), and only
+// that address is handed to kernels. Nothing in the workspace needs to start
+// at zero (the kernels write every partial before it is read and zero the
+// ticket counters themselves), so the array is used as found.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (the current
+// device for the null stream), resolved on the first call for that device
+// with it current.
+int scratch_for_stream(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  if (stream) {
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return fail(MGI_EINVAL, "invalid stream");
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return fail(MGI_ELAUNCH, "no current HIP device");
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail(MGI_EUNSUPPORTED, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return fail(MGI_ELAUNCH, "no current HIP device");
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return fail(MGI_ELAUNCH, "cannot select the stream's device");
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return fail(MGI_ELAUNCH, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MGI_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* mgi_last_error(void) { return g_err.c_str(); }
 
-int mgi_abi_version(void) { return 102; }
+int mgi_abi_version(void) { return 103; }
 
 int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                       int64_t split_tokens) {
@@ -303,14 +345,22 @@ size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t
   return workspace_layout(B, D, split_plan(B, H, D, S, M, split_tokens)).total;
 }
 
-int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
-                     const int64_t* q_strides, const void* k_pool, const void* v_pool,
-                     const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
-                     const void* block_tables, const int64_t* bt_strides, int bt_itype,
-                     const void* context_lens, int64_t cl_stride, int cl_itype, int64_t B,
-                     int64_t H, int64_t D, int64_t S, int64_t N, int64_t M, int64_t L,
-                     int64_t layer_idx, float scale, int64_t split_tokens, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The body of mgi_paged_decode and mgi_paged_decode_noalloc. When
+// `scratch_dev` >= 0 the workspace is that device's allocation-free scratch
+// (resolved here once the call is known to need it, after every check has
+// passed); otherwise it is the caller's `workspace`.
+int paged_decode_impl(void* out, const int64_t* out_strides, const void* q,
+                      const int64_t* q_strides, const void* k_pool, const void* v_pool,
+                      const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
+                      const void* block_tables, const int64_t* bt_strides, int bt_itype,
+                      const void* context_lens, int64_t cl_stride, int cl_itype, int64_t B,
+                      int64_t H, int64_t D, int64_t S, int64_t N, int64_t M, int64_t L,
+                      int64_t layer_idx, float scale, int64_t split_tokens, void* workspace,
+                      size_t workspace_bytes, bool use_scratch, void* stream) {
   using namespace mgi;
   g_err.clear();
   if (!out || !q || !k_pool || !v_pool || !block_tables || !context_lens)
@@ -413,6 +463,17 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   a.part_tokens = (int)sp.P;
   a.max_parts = plan.path == DecodePath::kFast ? (int)sp.max_parts : 1;
   if (plan.path == DecodePath::kFast && sp.n_partials > 0) {
+    if (use_scratch) {
+      if (ws.total > kScratchBytes)
+        return fail(MGI_EUNSUPPORTED, "this call needs " + std::to_string(ws.total) +
+                                          " bytes of split workspace, more than the " +
+                                          std::to_string(kScratchBytes) +
+                                          " bytes of mgi_paged_decode_noalloc's scratch; "
+                                          "use mgi_paged_decode with a workspace");
+      const int rc = scratch_for_stream(static_cast<hipStream_t>(stream), &workspace);
+      if (rc != MGI_OK) return rc;
+      workspace_bytes = kScratchBytes;
+    }
     if (!workspace) return fail(MGI_EWORKSPACE, "workspace required for split-context pass");
     if (workspace_bytes < ws.total)
       return fail(MGI_EWORKSPACE, "workspace smaller than mgi_paged_decode_workspace_bytes()");
@@ -443,6 +504,38 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   const hipError_t e = launch_paged_decode(a, dtype, plan, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MGI_ELAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
   return MGI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
+                     const int64_t* q_strides, const void* k_pool, const void* v_pool,
+                     const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
+                     const void* block_tables, const int64_t* bt_strides, int bt_itype,
+                     const void* context_lens, int64_t cl_stride, int cl_itype, int64_t B,
+                     int64_t H, int64_t D, int64_t S, int64_t N, int64_t M, int64_t L,
+                     int64_t layer_idx, float scale, int64_t split_tokens, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  return paged_decode_impl(out, out_strides, q, q_strides, k_pool, v_pool, k_pool_strides,
+                           v_pool_strides, dtype, block_tables, bt_strides, bt_itype, context_lens,
+                           cl_stride, cl_itype, B, H, D, S, N, M, L, layer_idx, scale, split_tokens,
+                           workspace, workspace_bytes, false, stream);
+}
+
+int mgi_paged_decode_noalloc(void* out, const int64_t* out_strides, const void* q,
+                             const int64_t* q_strides, const void* k_pool, const void* v_pool,
+                             const int64_t* k_pool_strides, const int64_t* v_pool_strides,
+                             int dtype, const void* block_tables, const int64_t* bt_strides,
+                             int bt_itype, const void* context_lens, int64_t cl_stride,
+                             int cl_itype, int64_t B, int64_t H, int64_t D, int64_t S, int64_t N,
+                             int64_t M, int64_t L, int64_t layer_idx, float scale,
+                             int64_t split_tokens, void* stream) {
+  return paged_decode_impl(out, out_strides, q, q_strides, k_pool, v_pool, k_pool_strides,
+                           v_pool_strides, dtype, block_tables, bt_strides, bt_itype, context_lens,
+                           cl_stride, cl_itype, B, H, D, S, N, M, L, layer_idx, scale, split_tokens,
+                           nullptr, 0, true, stream);
 }
 
 int mgi_kv_append(void* k_pool, void* v_pool, const int64_t* k_pool_strides,

@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "mgi_abi_version",
     "mgi_kv_append",
     "mgi_paged_decode",
+    "mgi_paged_decode_noalloc",
     "mgi_paged_decode_workspace_bytes",
     "mgi_paged_decode_split_tokens",
     "mgi_paged_decode_balanced_waves",
@@ -73,6 +74,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         _p, ctypes.c_size_t,               # workspace, bytes
         _p,                                # stream
     ]
+    lib.mgi_paged_decode_noalloc.restype = _i
+    lib.mgi_paged_decode_noalloc.argtypes = lib.mgi_paged_decode.argtypes[:-3] + [_p]
     lib.mgi_paged_decode_workspace_bytes.restype = ctypes.c_size_t
     lib.mgi_paged_decode_workspace_bytes.argtypes = [_i64] * 6
     lib.mgi_paged_decode_split_tokens.restype = _i64

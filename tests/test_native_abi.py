@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.lib()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mgi_abi_version() == 102
+    assert lib.mgi_abi_version() == 103
 
 
 def test_split_tokens_and_workspace_sizes():
@@ -205,3 +205,21 @@ def test_missing_library_raises_runtime_error(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "library_path", lambda: tmp_path / "libminivllm_hip.so")
     with pytest.raises(RuntimeError, match="not built"):
         _native.lib()
+
+
+def test_noalloc_decode_refuses_splits_beyond_its_scratch_on_host():
+    """mgi_paged_decode_noalloc holds 32 MiB of split workspace per device: a
+    call whose split needs more (here 256-token partitions of 64 x 32 heads x
+    4096-token tables, 272 MB) is refused before anything is resolved or
+    launched (the pointers are never dereferenced)."""
+    lib = _native.lib()
+    B, H, D, S, N, M = 64, 32, 128, 16, 20000, 256
+    assert lib.mgi_paged_decode_workspace_bytes(B, H, D, S, M, 16) > 32 << 20
+    pool = _i64(N * S * H * D, S * H * D, H * D, D, 1)
+    st3, st2 = _i64(H * D, D, 1), _i64(M, 1)
+    fake = 0x10000
+    st = lib.mgi_paged_decode_noalloc(fake, st3, fake, st3, fake, fake, pool, pool, _native.MGI_BF16,
+                                      fake, st2, 1, fake, 1, 1, B, H, D, S, N, M, 1, 0, 0.1, 16, None)
+    assert st == _native.MGI_EUNSUPPORTED
+    msg = lib.mgi_last_error().decode()
+    assert "scratch" in msg and str(32 << 20) in msg
