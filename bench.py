@@ -9,16 +9,22 @@ Prints ONE JSON line. `value` = algorithmic bytes / time per step, where the
 algorithmic bytes are
   sum_b ctx_b*H*D*e*2 + B*H*D*(e_q + e_out) + sum_b ceil(ctx_b/S)*e_idx + B*e_idx
 (valid tokens only; partial-block padding, split partials and the merge pass
-are overhead). Time comes from HIP events on torch's current stream, the
-stream the kernels launch on. `cpu_baseline` times the C restatement of the
-reference's online-softmax decode (oracle/paged_decode_oracle.c, fp32
-accumulation) on this host's cores over the same workload.
+are overhead). Time per step is the median of K per-call HIP event pairs on
+torch's current stream (the stream the kernels launch on), after W untimed
+calls, the region bracketed by device synchronisations. `cpu_baseline`
+times the C restatement of the reference's online-softmax decode
+(oracle/paged_decode_oracle.c, fp32 accumulation) on this host's cores over
+the same workload, with rows for the package's PyTorch online_v1 on the CPU
+(bf16 as-is and fp32-upcast), the KV append plus decode step, the long
+contexts, the small end-to-end model and a window of the full runtime.
 
 Extras (skipped with --no-extras) time other decode shapes, the KV append,
 the KV append plus decode attention of one high-batch step on one pool, the
 paged prefill kernel and same-GPU comparisons with the PyTorch backends.
 The end-to-end block (skipped with --no-e2e) runs the full runtime under
-recompute preemption and puts its decode tokens/s in `end_to_end`.
+recompute preemption and puts its decode tokens/s (generated tokens / wall
+seconds) in `end_to_end`, then runs it to completion in lock step against
+the PyTorch reference decode backend (skipped with --no-lockstep).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp32]
                        [--split-tokens P] [--no-extras] [--no-cpu-baseline]
@@ -68,6 +74,9 @@ def parse_args():
                          "vocab 32000, bf16, 256 requests, 128 output tokens) that reports decode "
                          "tokens/s")
     ap.add_argument("--e2e-requests", type=int, default=256)
+    ap.add_argument("--no-lockstep", action="store_true",
+                    help="skip the full runtime run in lock step against the PyTorch reference decode "
+                         "backend (about 2-3 minutes)")
     ap.add_argument("--prefill", action="store_true",
                     help="also time the paged prefill kernel (implied unless --no-extras)")
     ap.add_argument("--e2e-trace", action="store_true",
@@ -85,7 +94,9 @@ def log(msg: str) -> None:
 
 
 def time_steps(fn, steps: int, warmup: int) -> float:
-    """Milliseconds per call of fn, HIP events on the current stream."""
+    """Milliseconds per call of fn over `steps` back-to-back calls (one HIP
+    event pair around all of them, on the current stream): the throughput
+    rate, host overhead included when the host is slower than the GPU."""
     import torch
 
     for _ in range(warmup):
@@ -101,15 +112,43 @@ def time_steps(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def time_calls(fn, steps: int, warmup: int) -> dict:
+    """Per-call HIP event pairs on the current stream (the stream the kernels
+    launch on), `steps` calls after `warmup` untimed ones, bracketed by device
+    synchronisations: median, mean and min milliseconds per call, plus the
+    host wall time of the bracketed region per call."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, e in pairs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    ms = [s.elapsed_time(e) for s, e in pairs]
+    return {"median_ms": statistics.median(ms), "mean_ms": statistics.fmean(ms), "min_ms": min(ms),
+            "wall_ms": wall, "calls": steps}
+
+
 def decode_line(w, steps, warmup, split):
+    """One decode-attention call per step; the rate is algorithmic bytes over
+    the median of the per-call event timings."""
     from minivllm import hip_paged_decode as hpd
 
     fn = lambda: hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer,  # noqa: E731
                                                split_tokens=split)
-    ms = time_steps(fn, steps, warmup)
+    t = time_calls(fn, steps, warmup)
+    ms = t["median_ms"]
     nbytes = w.algorithmic_bytes()
     gbps = nbytes / (ms * 1e-3) / 1e9
-    return {"ms": round(ms, 5), "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+    return {"ms": round(ms, 5), "mean_ms": round(t["mean_ms"], 5), "min_ms": round(t["min_ms"], 5),
+            "wall_ms_per_call": round(t["wall_ms"], 5), "calls": t["calls"],
+            "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
             "alg_bytes": nbytes, "sum_ctx": int(w.ctx.sum()),
             "seq_per_s_per_layer": round(w.q.shape[0] / (ms * 1e-3), 1)}
 
@@ -129,11 +168,18 @@ def append_line(steps, warmup, dev):
     k = torch.randn(B, H, D, device=dev).to(torch.bfloat16)
     v = torch.randn(B, H, D, device=dev).to(torch.bfloat16)
     sl = slots.to(dev)
-    ms = time_steps(lambda: hpd.kv_append(pool, 0, k, v, sl), steps, warmup)
+    fn = lambda: hpd.kv_append(pool, 0, k, v, sl)  # noqa: E731
+    t = time_calls(fn, steps, warmup)
+    back_to_back = time_steps(fn, steps, warmup)
     n_valid = int((slots >= 0).sum())
     nbytes = n_valid * H * D * 2 * 2 * 2 + B * 8
-    return {"us": round(ms * 1e3, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "valid_rows": n_valid,
-            "alg_bytes": nbytes, "note": "launch-latency bound; working set is cache resident"}
+    ms = t["median_ms"]
+    return {"us": round(ms * 1e3, 2), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "back_to_back_us_per_call": round(back_to_back * 1e3, 2), "valid_rows": n_valid,
+            "alg_bytes": nbytes,
+            "note": "us: median per-call event pair, from before the Python wrapper to the end of the "
+                    "kernel (launch-latency bound; the working set is cache resident); back_to_back: "
+                    "calls issued in a loop, the host rate"}
 
 
 def c3_step_line(steps, warmup, dev):
@@ -179,7 +225,7 @@ def c3_step_line(steps, warmup, dev):
         hpd.kv_append(pool, 0, k_new, v_new, slots_d)
         hpd.paged_attention_batch_hip(q, pool, tables_d, lens_d, 0)
 
-    ms = time_steps(step, steps, warmup)
+    ms = time_calls(step, steps, warmup)["median_ms"]
     n_valid = int((~pad).sum())
     append_bytes = n_valid * H * D * 2 * 2 * 2 + B * 8
     attn_bytes = fx.DecodeWorkload(q, pool, tables_d, lens_d, 0, {}).algorithmic_bytes()
@@ -290,6 +336,59 @@ def e2e_line(n_requests: int, dev, graphs: bool, prefill_mode: str = "sdpa_v2",
         stats.update({"margins": margins, "prompt_lens": [len(s.prompt_tokens) for s in seqs],
                       "seq_ids": [s.seq_id for s in seqs]})
     return stats
+
+
+def e2e_lockstep_line(dev):
+    """The full runtime (256 requests, dim 2048 x 12 layers, bf16, recompute
+    preemption, sdpa_v2 prefill) run to completion twice in lock step, once
+    with the PyTorch reference decode backend and once with the HIP backend,
+    checking every iteration as tests/test_e2e_lockstep_gpu.py does over its
+    window (schedules, states, block tables, logits, KV; token divergence
+    only at near ties). Reports whether every check held, and how many token
+    streams are identical to the reference backend's at the end."""
+    import collections
+
+    import torch
+
+    import _e2e
+
+    spec = _e2e.RuntimeSpec()
+    model = e2e_model(dev)
+    model.set_prefill_fastpath_mode("sdpa_v2")
+    ls = _e2e.Lockstep(spec, model, _e2e.make_prompts(spec), dev, torch.bfloat16, **_e2e.C5_BF16_LOCKSTEP)
+    t0 = time.perf_counter()
+    err = None
+    try:
+        with torch.inference_mode():
+            while not ls.finished:
+                ls.step()
+                if ls.stats["steps"] % 25 == 0:
+                    log(f"lock step {ls.stats['steps']}: diverged {len(ls.diverged)} "
+                        f"preemptions {ls.stats['preemptions']} ({time.perf_counter() - t0:.0f} s)")
+                if ls.stats["steps"] >= 2000:
+                    raise AssertionError("the run did not finish in 2000 iterations")
+        ls.finish_checks()
+    except AssertionError as exc:
+        err = str(exc)
+    model.set_decode_attention_backend("hip")
+    st = ls.stats
+    same = sum(x.generated_tokens == ls.hip.by_id[x.seq_id].generated_tokens for x in ls.ref.seqs)
+    margins = collections.Counter(round(m, 6) for _, _, m in ls.diverged.values())
+    out = {"checks_passed": err is None, "error": err, "iterations": st["steps"],
+           "identical_token_streams_vs_reference_backend": f"{same}/{len(ls.ref.seqs)}",
+           "diverged_streams": len(ls.diverged),
+           "divergence_margins": {str(k): v for k, v in sorted(margins.items())},
+           "max_logit_abs": st["max_logit_abs"], "max_logit_fraction_of_bound": round(st["max_logit_ratio"], 3),
+           "max_kv_abs": st["max_kv_abs"], "max_kv_fraction_of_bound": round(st["max_kv_ratio"], 3),
+           "decode_rows_checked": st["decode_rows_checked"], "kv_token_rows_checked": st["kv_tokens_checked"],
+           "preemptions": st["preemptions"], "recomputed_sequences": len(st["recomputed_seqs"]),
+           "wall_s": round(time.perf_counter() - t0, 1),
+           "criterion": "logits and decode-written KV within 2^-6 + 2^-6*max|ref row|; layer-0 and "
+                        "prefill-written KV bit-identical; a stream may diverge only at a reference top-2 "
+                        "margin below twice its row's bound and then leaves the logit/KV checks"}
+    del ls
+    torch.cuda.empty_cache()
+    return out
 
 
 PEAK_BF16_TFLOPS = 2500.0
@@ -502,25 +601,161 @@ def e2e_c1_speedup(dev):
     return {"min_speedup": min(sp), "max_speedup": max(sp), "cases": rows}
 
 
-def cpu_baseline(w):
+def cpu_threads() -> tuple[int, int]:
+    """Threads of the CPU baseline: every core of this process's affinity set,
+    capped by OMP_NUM_THREADS when the environment sets it (the host share a
+    GPU box allots to its one GPU). Returns (threads used, affinity cores)."""
+    aff = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS") or 0)
+    return (min(aff, share) if share > 0 else aff), aff
+
+
+def _seconds(fn, warmup: int, repeats: int) -> float:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_baseline(w, dev) -> dict:
+    """The decode path on this host's cores, beside the GPU figures. The main
+    figure is the C restatement of paged_attention_batch_online_v1
+    (oracle/paged_decode_oracle.c, fp32 accumulation) on the decode workload;
+    `rows` add the package's PyTorch online_v1 (the "reference" decode
+    backend, the reference's own CPU path) on the same input as-is in bf16
+    and upcast to fp32, the KV append plus decode step at B=256, the long
+    contexts (one repeat), the small end-to-end model and a window of the
+    full runtime. Every row names its sample, threads and repeats."""
+    import torch
+
+    import _e2e
+    import _fixtures as fx
+    from minivllm.paged_attention_batch import paged_attention_batch_online_v1
     from oracle import c_oracle
 
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
-    args = w.compact_host()
-    times = []
-    for i in range(4):  # 1 warmup + 3 timed
+    threads, aff = cpu_threads()
+    torch.set_num_threads(threads)
+    host = {"cores": threads, "affinity_cores": aff, "cpu": _cpu_model()}
+    rows = {}
+
+    def port_row(wl, repeats, name, desc):
+        args = wl.compact_host()
+        sec = _seconds(lambda: c_oracle.paged_decode(*args, acc_double=False, threads=threads),
+                       1 if repeats > 1 else 0, repeats)
+        rows[name] = {"value": round(wl.algorithmic_bytes() / sec / 1e9, 3), "unit": "GB/s",
+                      "ms": round(sec * 1e3, 2), "kind": "port", **host,
+                      "sample": f"{desc} through oracle/paged_decode_oracle.c (fp32 accumulation); "
+                                f"median of {repeats}" + (" after 1 warmup" if repeats > 1 else "")}
+        log(f"cpu {name}: {rows[name]}")
+
+    port_row(w, 3, "decode_port", f"the decode workload (B={w.q.shape[0]}, sum ctx={int(w.ctx.sum())}, "
+                                   f"{w.meta['dtype']})")
+
+    cw = w.compact_cpu()
+    with torch.inference_mode():
+        for name, dt in (("decode_online_v1_torch", None), ("decode_online_v1_torch_fp32_upcast", torch.float32)):
+            q, pool = cw.q, cw.pool
+            if dt is not None:
+                q = q.to(dt)
+                from minivllm.kv_block_pool import KVBlockPool
+                pool = KVBlockPool(1, cw.pool.num_blocks, cw.pool.block_size, cw.pool.n_head, cw.pool.head_dim,
+                                   dtype=dt)
+                pool.k.copy_(cw.pool.k)
+                pool.v.copy_(cw.pool.v)
+            sec = _seconds(lambda: paged_attention_batch_online_v1(q, pool, cw.tables, cw.ctx, 0), 1, 3)
+            nbytes = fx.DecodeWorkload(q, pool, cw.tables, cw.ctx, 0, {}).algorithmic_bytes()
+            rows[name] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "ms": round(sec * 1e3, 1),
+                          "kind": "port", **host,
+                          "sample": "the same decode workload through minivllm.paged_attention_batch."
+                                    "paged_attention_batch_online_v1 on CPU tensors (the reference's per-"
+                                    "block gather/mask/online loop, torch ops in "
+                                    f"{str(q.dtype).replace('torch.', '')}); median of 3 after 1 warmup"}
+            log(f"cpu {name}: {rows[name]}")
+            del q, pool
+    del cw
+
+    # KV append + decode at B=256, ctx U[128, 2048]: torch index_put_ of the
+    # 10%-padded rows, then the C restatement over the appended contexts.
+    w3 = fx.make_decode_workload(256, 32, 128, 16, 32768, 128, 2048, torch.bfloat16, dev, seed=0, poison=False)
+    c3 = w3.compact_cpu()
+    g = torch.Generator().manual_seed(0)
+    pad = torch.zeros(256, dtype=torch.bool)
+    pad[torch.randperm(256, generator=g)[:25]] = True
+    last = c3.ctx - 1
+    slots = c3.tables[torch.arange(256), last // 16] * 16 + last % 16
+    slots = torch.where(pad, torch.full_like(slots, -1), slots)
+    k_new = torch.randn(256, 32, 128, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(256, 32, 128, generator=g).to(torch.bfloat16)
+    args = c3.compact_host()
+
+    def c3_step():
+        keep = slots >= 0
+        s = slots[keep]
+        c3.pool.k[0, s // 16, s % 16] = k_new[keep]
+        c3.pool.v[0, s // 16, s % 16] = v_new[keep]
+        c_oracle.paged_decode(*args, acc_double=False, threads=threads)
+
+    sec = _seconds(c3_step, 1, 3)
+    nbytes = w3.algorithmic_bytes() + int((~pad).sum()) * 32 * 128 * 2 * 2 * 2
+    rows["append_plus_decode_B256"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
+                                       "ms": round(sec * 1e3, 2), "kind": "port", **host,
+                                       "sample": "KV append (torch index_put_ of 231 rows, 25 padding rows "
+                                                 "skipped) then decode over B=256 ctx U[128,2048] bf16 through "
+                                                 "oracle/paged_decode_oracle.c; median of 3 after 1 warmup"}
+    log(f"cpu append_plus_decode_B256: {rows['append_plus_decode_B256']}")
+    del w3, c3, args
+    torch.cuda.empty_cache()
+
+    w4 = fx.make_decode_workload(8, 32, 128, 16, 65536, 32768, 131072, torch.bfloat16, dev, seed=0, poison=False)
+    port_row(w4, 1, "longctx_port", "the long-context workload (B=8, ctx U[32768,131072], bf16), one repeat,")
+    del w4
+    torch.cuda.empty_cache()
+
+    # The small end-to-end model on the CPU with the reference decode backend.
+    t_all, toks = 0.0, 0
+    for case in _e2e.GOLDEN_C1["cases"]:
         t0 = time.perf_counter()
-        c_oracle.paged_decode(*args, acc_double=False, threads=cores)
-        if i:
-            times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
-    return {"value": round(w.algorithmic_bytes() / sec / 1e9, 3), "unit": "GB/s", "cores": cores,
-            "kind": "port", "ms": round(sec * 1e3, 2),
-            "sample": (f"the full decode workload (B={w.q.shape[0]}, sum ctx={int(w.ctx.sum())}, "
-                       f"{w.meta['dtype']}) through oracle/paged_decode_oracle.c, a C restatement of "
-                       "paged_attention_batch_online_v1 with fp32 accumulation; median of 3 after "
-                       "1 warmup"),
-            "cpu": _cpu_model()}
+        tokens, _ = _e2e.run_c1(case, "cpu", "reference")
+        t_all += time.perf_counter() - t0
+        toks += sum(len(t) for t in tokens)
+    rows["e2e_small_model"] = {"value": round(toks / t_all, 1), "unit": "generated tokens/s",
+                               "s": round(t_all, 3), "kind": "port", **host,
+                               "sample": "the Mini-GPT end-to-end runs (dim 256, 4 layers, fp32; prompts "
+                                         "128/256 x batch 1/4; budget 64; 8 greedy tokens), all four cases "
+                                         "once, reference decode backend, sdpa_v2 prefill, on the CPU"}
+    log(f"cpu e2e_small_model: {rows['e2e_small_model']}")
+
+    # A labelled window of the full runtime: its first iterations (prefill
+    # dominated), as the runtime runs them, on the CPU.
+    spec = _e2e.RuntimeSpec()
+    model = _e2e.make_model(spec, "cpu", torch.bfloat16)
+    model.set_decode_attention_backend("reference")
+    rt, seqs = _e2e.make_runtime(spec, model, _e2e.make_prompts(spec), "cpu", torch.bfloat16)
+    n_iter = 3
+    t0 = time.perf_counter()
+    with torch.inference_mode():
+        for _ in range(n_iter):
+            rt.step()
+    sec = time.perf_counter() - t0
+    summ = rt.metrics_summary()
+    rows["full_runtime_window"] = {"value": round(summ["scheduled_tokens"] / sec, 1),
+                                   "unit": "scheduled tokens/s", "s": round(sec, 2), "kind": "port", **host,
+                                   "iterations": n_iter, "prefill_tokens": summ["prefill_tokens"],
+                                   "decode_tokens": summ["decode_tokens"],
+                                   "sample": f"iterations 1-{n_iter} of the full runtime (dim 2048 x 12 layers, "
+                                             "vocab 32000, bf16, 256 requests; prefill dominated) on the CPU, "
+                                             "reference decode backend, sdpa_v2 prefill; a window, not the "
+                                             "whole run"}
+    log(f"cpu full_runtime_window: {rows['full_runtime_window']}")
+    del rt, seqs, model
+
+    main = rows["decode_port"]
+    return {"value": main["value"], "unit": "GB/s", "cores": threads, "kind": "port", "sample": main["sample"],
+            "ms": main["ms"], "affinity_cores": aff, "cpu": host["cpu"], "rows": rows}
 
 
 def cpu_prefill_baseline(start: int = 0, T: int = 512, H: int = 16, D: int = 128, S: int = 16):
@@ -545,9 +780,9 @@ def cpu_prefill_baseline(start: int = 0, T: int = 512, H: int = 16, D: int = 128
             times.append(time.perf_counter() - t0)
     sec = statistics.median(times)
     flops = 4 * H * D * (T * start + T * (T + 1) // 2)
-    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or len(os.sched_getaffinity(0))
+    threads, _ = cpu_threads()
     return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "ms": round(sec * 1e3, 2),
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", "cpu": _cpu_model(),
             "sample": f"one prefill chunk (start {start}, T {T}, H {H}, D {D}) through "
                       "oracle.paged_decode.paged_prefill in float32; median of 2 after 1 warmup"}
 
@@ -703,12 +938,21 @@ def main() -> None:
                 log(f"e2e {key}: {extras[key]}")
             extras["decode_step_latency_eager_vs_graph"] = decode_step_latency(dev)
             extras["decode_metadata_prep"] = metadata_prep_line(dev)
+            if not args.no_lockstep and args.e2e_requests == 256:
+                log("e2e: full runtime in lock step, reference decode backend vs HIP (about 2-3 minutes)")
+                extras["e2e_lockstep_vs_reference_backend"] = e2e_lockstep_line(dev)
+                log(f"e2e lock step: {extras['e2e_lockstep_vs_reference_backend']}")
             hip = extras["e2e_runtime_bf16_preemption_hip_prefill"]
             hip_g = extras["e2e_runtime_bf16_preemption_hip_prefill_graphs"]
-            e2e_summary = {"decode_tokens_per_s": hip["decode_tok_s_in_decode_phase"],
-                           "output_tokens_per_s": hip["output_tok_s"],
-                           "decode_tokens_per_s_with_graphs": hip_g["decode_tok_s_in_decode_phase"],
-                           "output_tokens_per_s_with_graphs": hip_g["output_tok_s"],
+            e2e_summary = {"decode_tokens_per_s": hip["output_tok_s"],
+                           "decode_tokens_per_s_with_graphs": hip_g["output_tok_s"],
+                           "decode_tokens_per_s_definition":
+                               "generated tokens / wall seconds of the whole run, prefill included "
+                               "(output_tok_s of experiments/gpu_e2e_runtime.py:198)",
+                           "decode_phase_tokens_per_s": hip["decode_tok_s_in_decode_phase"],
+                           "decode_phase_tokens_per_s_with_graphs": hip_g["decode_tok_s_in_decode_phase"],
+                           "decode_phase_tokens_per_s_definition":
+                               "decode tokens / seconds spent inside decode steps only",
                            "workload": "full runtime, 256 requests, MiniGPT dim 2048 x 12 layers, bf16, "
                                        "HIP decode + HIP prefill, recompute preemption (eager; "
                                        "'with_graphs': decode steps of <= 128 rows replay HIP graphs)"}
@@ -722,8 +966,8 @@ def main() -> None:
         cpu = None
         if not args.no_cpu_baseline:
             log("timing CPU baseline")
-            cpu = cpu_baseline(w)
-            cpu["prefill"] = cpu_prefill_baseline()
+            cpu = cpu_baseline(w, dev)
+            cpu["rows"]["prefill_chunk"] = cpu_prefill_baseline()
             log(f"cpu: {cpu}")
 
     workload_tag = f"decode_{args.workload}_{args.dtype}_B{B}_H{H}_D{D}_ctx{ctx_lo}-{ctx_hi}"
@@ -736,6 +980,7 @@ def main() -> None:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": main_line["ms"],
+        "ms_per_step_mean": main_line["mean_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

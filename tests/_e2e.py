@@ -256,6 +256,15 @@ def _token_slots(seq: SequenceState, S: int) -> list[int]:
     return [t[p // S] * S + p % S for p in range(seq.length)]
 
 
+# Lock-step criterion of the full configuration in bf16 (see Lockstep and
+# test_e2e_lockstep_gpu.py), scaled by each row's largest magnitude: logits
+# and decode-written KV within 2^-6 + 2^-6 * max|row| (four bf16 ulps of the
+# row's largest entry, plus 2^-6); a token may diverge only where the
+# reference's top-2 margin is below twice its row's logit bound.
+C5_BF16_LOCKSTEP = dict(logit_tol=(2.0 ** -6, 2.0 ** -6), tie_margin=None, kv_tol=(2.0 ** -6, 2.0 ** -6),
+                        row_scaled=True)
+
+
 class Lockstep:
     """The reference runtime and the HIP runtime stepped alternately over one
     model, one request set and two KV pools of the same size, as
@@ -270,32 +279,40 @@ class Lockstep:
         counts -- the schedule is token-independent, so this holds even
         after a token stream diverges;
       * decode logits of every row whose inputs still agree within
-        ``logit_tol`` (|hip - ref| <= atol + rtol * |ref|);
+        ``logit_tol`` = (atol, rtol): |hip - ref| <= atol + rtol * |ref|
+        elementwise, or, with ``row_scaled``, atol + rtol * max|ref row|
+        (rounding of the hidden state moves every logit of a row in
+        proportion to the row's scale, not to the logit's own size);
       * greedy tokens identical, except that a stream may diverge where the
-        reference's top-2 logit margin is below ``tie_margin``; the diverged
-        sequence is left out of the logit and KV checks from then on (its
-        inputs differ);
+        reference's top-2 logit margin is below ``tie_margin`` (None: twice
+        that row's logit bound, the largest gap two logits each moved by the
+        bound can close); the diverged sequence is left out of the logit and
+        KV checks from then on (its inputs differ);
       * logical KV of every active, not diverged sequence read through its
         block table: bit-identical in layer 0 (its input is the token and
         position embedding alone) and at every position the current prefill
         wrote (prefill is shared and deterministic), within ``kv_tol`` at
         positions decode wrote in later layers (the decode attention outputs
-        differ in rounding). ``kv_tol=None`` checks through
+        differ in rounding; ``row_scaled`` scales by each token's [H, D] row
+        in that layer). ``kv_tol=None`` checks through
         KVBlockPool.gather_sequence on the host instead, with ``kv_tol``
-        replaced by ``logit_tol`` everywhere, as the reference harness does.
+        replaced by ``logit_tol`` elementwise, as the reference harness does.
 
     Statistics of every check accumulate in ``stats``.
     """
 
     def __init__(self, spec: RuntimeSpec, model: MiniGPT, prompts, device, dtype, *,
-                 logit_tol: tuple[float, float], tie_margin: float, kv_tol: tuple[float, float] | None):
+                 logit_tol: tuple[float, float], tie_margin: float | None, kv_tol: tuple[float, float] | None,
+                 row_scaled: bool = False):
         self.model = model
         self.logit_tol, self.tie_margin, self.kv_tol = logit_tol, tie_margin, kv_tol
+        self.row_scaled = row_scaled
         self.ref = _Probe(*make_runtime(spec, model, prompts, device, dtype))
         self.hip = _Probe(*make_runtime(spec, model, prompts, device, dtype))
         self.diverged: dict[str, tuple[int, int, float]] = {}   # seq_id -> (step, token index, margin)
-        self.stats = {"steps": 0, "decode_rows_checked": 0, "max_logit_abs": 0.0, "max_logit_excess": 0.0,
-                      "kv_tokens_checked": 0, "kv_exact_tokens": 0, "max_kv_abs": 0.0, "max_kv_excess": 0.0,
+        # max_*_ratio: the largest deviation as a fraction of its bound (<= 1 passes).
+        self.stats = {"steps": 0, "decode_rows_checked": 0, "max_logit_abs": 0.0, "max_logit_ratio": 0.0,
+                      "kv_tokens_checked": 0, "kv_exact_tokens": 0, "max_kv_abs": 0.0, "max_kv_ratio": 0.0,
                       "preemptions": 0, "recomputed_seqs": set()}
 
     @property
@@ -346,11 +363,12 @@ class Lockstep:
                 rows = torch.tensor(keep, device=a.logits.device)
                 ra, rb = a.logits.index_select(0, rows), b.logits.index_select(0, rows)
                 diff = (ra - rb).abs()
-                excess = (diff - (atol + rtol * ra.abs())).max().item()
+                scale = ra.abs().amax(dim=1, keepdim=True) if self.row_scaled else ra.abs()
+                ratio = (diff / (atol + rtol * scale)).max().item()
                 self.stats["max_logit_abs"] = max(self.stats["max_logit_abs"], diff.max().item())
-                self.stats["max_logit_excess"] = max(self.stats["max_logit_excess"], excess)
+                self.stats["max_logit_ratio"] = max(self.stats["max_logit_ratio"], ratio)
                 self.stats["decode_rows_checked"] += len(keep)
-                if excess > 0:
+                if ratio > 1:
                     raise AssertionError(f"step {step}: decode logits differ by {diff.max().item():.4g} "
                                          f"(tolerance atol {atol} + rtol {rtol} * |ref|)")
         # Tokens: every stream not yet diverged must agree; a new divergence
@@ -367,9 +385,12 @@ class Lockstep:
             row = a.logits[a.decoded.index(x.seq_id)]
             top = torch.topk(row, 2).values.tolist()
             margin = top[0] - top[1]
-            if margin >= self.tie_margin:
+            allowed = self.tie_margin
+            if allowed is None:
+                allowed = 2 * (atol + rtol * row.abs().max().item())
+            if margin >= allowed:
                 raise AssertionError(f"step {step}: {x.seq_id} token {k} differs at reference top-2 "
-                                     f"margin {margin:.4g} (allowed only below {self.tie_margin})")
+                                     f"margin {margin:.4g} (allowed only below {allowed:.4g})")
             self.diverged[x.seq_id] = (step, k, margin)
 
     def _check_kv(self, step: int) -> None:
@@ -413,11 +434,11 @@ class Lockstep:
                                          f"{int(bad.sum())} prefill-written or layer-0 positions")
                 uf, wf = u.float(), w.float()
                 diff = (uf - wf).abs()
-                excess = (diff - (atol + rtol * uf.abs())).amax(dim=(1, 2))
-                worst = excess.max().item()
+                scale = uf.abs().amax(dim=(1, 2), keepdim=True) if self.row_scaled else uf.abs()
+                worst = (diff / (atol + rtol * scale)).max().item()
                 self.stats["max_kv_abs"] = max(self.stats["max_kv_abs"], diff.max().item())
-                self.stats["max_kv_excess"] = max(self.stats["max_kv_excess"], worst)
-                if worst > 0:
+                self.stats["max_kv_ratio"] = max(self.stats["max_kv_ratio"], worst)
+                if worst > 1:
                     raise AssertionError(f"step {step}: layer {layer} logical KV differs by "
                                          f"{diff.max().item():.4g} (tolerance atol {atol} + rtol {rtol} * |ref|)")
         self.stats["kv_tokens_checked"] += len(slots)

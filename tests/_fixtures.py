@@ -151,6 +151,21 @@ class DecodeWorkload:
         return int(ctx.sum()) * H * D * e * 2 + B * H * D * 2 * e + \
             int(((ctx + S - 1) // S).sum()) * e_idx + B * self.ctx.element_size()
 
+    def compact_cpu(self) -> "DecodeWorkload":
+        """The same workload on the CPU, its pool holding only the used blocks
+        (tables remapped): the input of CPU baselines."""
+        tables = self.tables.cpu()
+        used = torch.unique(tables[tables >= 0])
+        remap = torch.full((self.pool.num_blocks,), -1, dtype=torch.int64)
+        remap[used] = torch.arange(used.numel())
+        new_tables = torch.where(tables >= 0, remap[tables.clamp(min=0)], tables)
+        dev_used = used.to(self.pool.k.device)
+        L, N, S, H, D = self.pool.k.shape
+        pool = KVBlockPool(1, used.numel(), S, H, D, dtype=self.pool.dtype)
+        pool.k.copy_(self.pool.k[self.layer, dev_used][None])
+        pool.v.copy_(self.pool.v[self.layer, dev_used][None])
+        return DecodeWorkload(self.q.cpu(), pool, new_tables, self.ctx.cpu(), 0, dict(self.meta))
+
     def compact_host(self):
         """Host copies of only the used blocks (tables remapped) for the oracle."""
         tables = self.tables.cpu()

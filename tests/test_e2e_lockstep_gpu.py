@@ -9,25 +9,26 @@ logical KV of every active sequence are compared (see _e2e.Lockstep).
 * Full configuration, bf16 (dim 2048 x 16 heads x 12 layers, vocab 32000,
   256 requests with lognormal prompts of mean 512 capped at 4096, 128 output
   tokens, pool at 60% of peak demand, max_running 256, token budget 2048,
-  prefill "sdpa_v2" in both runtimes): a window of C5_STEPS iterations that
-  runs through the first recompute preemptions (iteration 49 onwards) and
-  the first recompute prefills. The reference backend keeps its running
-  softmax state in bf16 while the HIP kernel accumulates in fp32, so:
-    - decode logits agree within |hip - ref| <= C5_LOGIT_ATOL +
-      C5_LOGIT_RTOL * |ref|: one bf16 ulp at magnitude 4 (2^-5) plus four
-      bf16 ulps relative (2^-6 * |ref|). Measured on MI355X: at most 2^-5
-      over 4862 decode rows;
-    - a token stream may diverge only where the reference's top-2 logit
-      margin is below C5_TIE_MARGIN = 2^-4, twice the largest logit
-      deviation measured (a gap that small can flip when each logit moves by
-      one ulp). Measured: divergences only at margins 0, 2^-6 and 2^-5
-      (ties and one-ulp gaps of bf16 logits);
+  prefill "sdpa_v2" in both runtimes), run to completion (283 iterations, 62
+  preemptions). The reference backend keeps its running softmax state in
+  bf16 (rounded at every block) while the HIP kernel accumulates in fp32, so
+  the two differ by bf16 rounding that grows with the context; the criterion
+  is stated in bf16 units of each row's largest entry
+  (_e2e.C5_BF16_LOCKSTEP):
+    - decode logits: |hip - ref| <= 2^-6 + 2^-6 * max|ref row| (four bf16
+      ulps of the row's largest logit, plus 2^-6);
+    - a token stream may diverge only where the reference's top-2 margin is
+      below twice its row's bound (two logits each moved by the bound can
+      close that gap); it then leaves the logit and KV checks;
     - logical KV: bit-identical in layer 0 and at prefill-written positions,
-      within C5_KV_ATOL + C5_KV_RTOL * |ref| (the logit bound) at
-      decode-written positions of later layers. Measured: at most 0.0234.
+      within the same bound (per token row of one layer) at decode-written
+      positions of later layers.
+  Measured on MI355X over the whole run: max |dlogit| 0.039, max |dKV|
+  0.031; divergences only at margins 0, 2^-6 and 2^-5.
 * Reduced configuration in fp32 (12 requests, dim 512, 2 layers), run to
   completion with the reference harness's own tolerances (atol 2e-5, rtol
-  2e-4) on logits and on KVBlockPool.gather_sequence, and identical tokens.
+  2e-4, elementwise) on logits and on KVBlockPool.gather_sequence, and
+  identical tokens.
 """
 from __future__ import annotations
 
@@ -42,10 +43,7 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 C5 = _e2e.RuntimeSpec()
-C5_STEPS = 64
-C5_LOGIT_ATOL, C5_LOGIT_RTOL = 2.0 ** -5, 2.0 ** -6
-C5_TIE_MARGIN = 2.0 ** -4
-C5_KV_ATOL, C5_KV_RTOL = 2.0 ** -5, 2.0 ** -6
+C5_MAX_STEPS = 400
 
 REDUCED = _e2e.RuntimeSpec(n_requests=12, prompt_mean=96, prompt_cap=320, output_len=12, n_embd=512, n_head=4,
                            n_layer=2, vocab=2048, max_running=12, token_budget=256, seed=3)
@@ -55,27 +53,32 @@ def _report(ls: _e2e.Lockstep, t0: float) -> str:
     s = ls.stats
     return (f"step {s['steps']} decode_rows {s['decode_rows_checked']} preemptions {s['preemptions']} "
             f"recomputed {len(s['recomputed_seqs'])} diverged {len(ls.diverged)} "
-            f"max|dlogit| {s['max_logit_abs']:.4g} max|dKV| {s['max_kv_abs']:.4g} "
+            f"max|dlogit| {s['max_logit_abs']:.4g} ({s['max_logit_ratio']:.2f} of bound) "
+            f"max|dKV| {s['max_kv_abs']:.4g} ({s['max_kv_ratio']:.2f} of bound) "
             f"kv_tokens {s['kv_tokens_checked']} ({time.perf_counter() - t0:.1f} s)")
 
 
 @pytest.mark.timeout(900)
-def test_lockstep_full_runtime_bf16_window():
+def test_lockstep_full_runtime_bf16_to_completion():
     torch.backends.cuda.matmul.allow_tf32 = False
     print("  building the full configuration (dim 2048 x 12 layers, 256 requests, bf16)", flush=True)
     prompts = _e2e.make_prompts(C5)
     model = _e2e.make_model(C5, DEV, torch.bfloat16)
-    ls = _e2e.Lockstep(C5, model, prompts, DEV, torch.bfloat16, logit_tol=(C5_LOGIT_ATOL, C5_LOGIT_RTOL),
-                       tie_margin=C5_TIE_MARGIN, kv_tol=(C5_KV_ATOL, C5_KV_RTOL))
+    ls = _e2e.Lockstep(C5, model, prompts, DEV, torch.bfloat16, **_e2e.C5_BF16_LOCKSTEP)
     t0 = time.perf_counter()
     with torch.inference_mode():
-        for _ in range(C5_STEPS):
+        while not ls.finished:
             ls.step()
-            print("  " + _report(ls, t0), flush=True)
-    print(f"  diverged streams (seq, step, token, reference top-2 margin): "
-          f"{sorted((k, *v) for k, v in ls.diverged.items())}", flush=True)
-    assert ls.stats["preemptions"] > 0, "the window must reach recompute preemption"
-    assert ls.stats["recomputed_seqs"], "the window must reach a recompute prefill"
+            if ls.stats["steps"] % 10 == 0:
+                print("  " + _report(ls, t0), flush=True)
+            assert ls.stats["steps"] < C5_MAX_STEPS
+    print("  " + _report(ls, t0), flush=True)
+    same = sum(x.generated_tokens == ls.hip.by_id[x.seq_id].generated_tokens for x in ls.ref.seqs)
+    print(f"  identical token streams: {same}/{len(ls.ref.seqs)}; divergence margins: "
+          f"{sorted(m for _, _, m in ls.diverged.values())}", flush=True)
+    ls.finish_checks()
+    assert ls.stats["preemptions"] > 0, "the run must reach recompute preemption"
+    assert ls.stats["recomputed_seqs"], "the run must reach a recompute prefill"
     assert ls.stats["decode_rows_checked"] > 0
 
 
