@@ -22,6 +22,8 @@
 // inputs use v_mfma_f32_16x16x32_bf16 / _f16 with P rounded to the input
 // type for the PV product, fp32 inputs use v_mfma_f32_16x16x4_f32 (full fp32
 // products).
+#include <cstdlib>
+
 #include "mgi_common.h"
 #include "mgi_internal.h"
 #include "minivllm_hip.h"
@@ -551,14 +553,657 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
   }
 }
 
+// ------------------------------------------------------------------------
+// Direct-to-LDS variant (2-byte types, head dims 64 and 128, power-of-two
+// block sizes of at least 16). Same work split, grid mapping, numerics and
+// outputs as paged_prefill_mfma; what changes is how key tiles reach the
+// matrix cores and how little per-tile work the wavefronts spend on it:
+//   * A key tile is 64 keys = four 16-key granules, and a granule lies in one
+//     pool block (S is a power of two >= 16). The workgroup keeps a window of
+//     the block table in LDS as one int per granule: G = block * (S / 16) +
+//     (offset in block) / 16, or -1 where the table entry is invalid or the
+//     granule starts past the chunk. One 16-byte LDS read yields a tile's
+//     four granules; what follows from them is wave-uniform scalar work.
+//   * K and V tiles are copied from HBM straight into LDS by 16-byte
+//     global_load_lds copies (one instruction moves 1 KiB: RPG whole key
+//     rows); each wavefront copies whole granules. When a tile's granules are
+//     all valid and inside the chunk, a copy is the granule's base address in
+//     scalar registers plus a per-lane 32-bit offset fixed for the whole
+//     loop. Otherwise each lane picks its source row, and keys past the
+//     chunk, invalid granules and head dims past D read a zero row.
+//   * Rows store their 16-byte chunk c at c ^ ks(r) (K) and c ^ vs(r) (V),
+//     swizzles chosen by measuring these kernels' read sequences on MI355X:
+//     ks(r) = (r & 3) | ((r >> 1) & (CPR - 4)); vs(r) = 2 (r & 3) |
+//     8 ((r >> 3) & 1) for 16-chunk rows, 2 (r & 3) for 8-chunk rows.
+//   * S^T = K Q^T reads the A operand (16 keys x 8 head dims per lane) as one
+//     16-byte row read; the A rows of key block kb = 2c + h are the keys
+//     32c + 8(r/4) + 4h + r%4, so the S^T column a lane holds for blocks 2c
+//     and 2c+1 is exactly the 8 keys 32c + 8g .. 32c + 8g + 7 that the PV
+//     product takes as its B operand (P^T), packed in register order.
+//   * O^T += V^T P^T reads its A operand (V^T: 16 head dims x those 8 keys)
+//     with two ds_read_b64_tr_b16: in each 16-lane group, lane i receives
+//     element i % 4 of the 4-element chunks addressed by lanes 4j + i/4,
+//     j = 0..3 (the instruction's lane layout, measured on MI355X), so lanes
+//     addressing V rows (keys) 8g + 4u + j at head dims 16db + 4q give lane i
+//     head dim 16db + i of four consecutive keys.
+//   * Two stages: tile t + 1 is copied while tile t is computed, with one
+//     barrier per tile. The loop body exists once per stage, so the LDS
+//     offsets of the operand reads are immediates. The copies are inline
+//     assembly, so the compiler adds no waits of its own for them; the loop
+//     waits for them explicitly (each wave's copies, then the barrier).
+template <int CPR>
+__device__ __forceinline__ int k_swz(int row) {
+  return (row & 3) | ((row >> 1) & (CPR - 4));
+}
+template <int CPR>
+__device__ __forceinline__ int v_swz(int row) {
+  return CPR == 16 ? (2 * (row & 3)) | (8 * ((row >> 3) & 1)) : 2 * (row & 3);
+}
+
+// Source of the zero rows the copies read for keys that must contribute nothing.
+__device__ __align__(16) const unsigned char kZeroRow[512] = {0};
+
+template <typename T> struct TrRead;
+template <> struct TrRead<bf16_t> {
+  typedef __bf16 v4 __attribute__((ext_vector_type(4)));
+  __device__ static __forceinline__ uint2 read(const unsigned char* p) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                         (__attribute__((address_space(3))) v4*)(p)));
+  }
+};
+template <> struct TrRead<f16_t> {
+  typedef __fp16 v4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+  __device__ static __forceinline__ uint2 read(const unsigned char* p) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                         (__attribute__((address_space(3))) v4*)(p)));
+  }
+};
+
+// One 16-byte copy per lane from global memory into LDS at lds_base + 16 *
+// lane (lds_base wave-uniform, through M0): from a per-lane address, or from a
+// wave-uniform base plus a per-lane 32-bit offset.
+__device__ __forceinline__ void copy16_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base) : "memory");
+}
+__device__ __forceinline__ void copy16_to_lds(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory");
+}
+
+// Waits until at most N of this wave's vector-memory instructions are
+// outstanding and all its LDS and scalar memory instructions are done, then
+// joins the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N) expcnt(7) lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)(p);
+}
+
+constexpr int kGranuleWindow = 1024;  // 16-key granules of the block table a workgroup keeps in LDS
+
+template <int V> struct Stage {
+  static constexpr int value = V;
+};
+
+// Calls f(Stage<I>{}) for I = B .. E - 1.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(Stage<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// GROUPS = 2 splits the workgroup's wavefronts into two groups of WAVES that
+// cover the same query rows: group r takes the key tiles t with t % 2 == r,
+// each through its own STAGES tile buffers, and at the end group 1 hands its
+// softmax state (running max, partial sums, unnormalised output) to group 0
+// through LDS, which merges and stores. A wavefront can then own 32 query rows
+// (each K and V read from LDS feeds two products) while two wavefronts share
+// every SIMD.
+template <typename T, int DP, int WAVES, int QPW, int STAGES, int GROUPS>
+__global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const PrefillArgs a) {
+  static_assert(sizeof(T) == 2 && (DP == 64 || DP == 128), "2-byte types, head dim 64 or 128");
+  static_assert(WAVES == 2 || WAVES == 4 || WAVES == 8, "two, four or eight wavefronts per group");
+  static_assert(STAGES >= 2 && STAGES <= 4, "two to four tiles in flight");
+  static_assert(GROUPS == 1 || GROUPS == 2, "one or two groups");
+  constexpr int ROWB = DP * 2;               // bytes per key row
+  constexpr int CPR = DP / 8;                // 16-byte chunks per key row
+  constexpr int TILEB = kTileKeys * ROWB;    // bytes per K (or V) tile
+  constexpr int RPG = 1024 / ROWB;           // key rows per copy
+  constexpr int GPW = TILEB / 1024 / WAVES;  // copies per wave and tile (K or V)
+  static_assert(GPW >= 1 && GPW * WAVES * 1024 == TILEB, "copies split evenly over the wavefronts");
+  constexpr int RW = GPW * RPG;              // tile rows per wave
+  constexpr int GRW = RW >= 16 ? RW / 16 : 1;  // granules a wave's rows lie in
+  constexpr int CPGW = GPW / GRW;            // copies per such granule
+  static_assert(2 * GPW * (STAGES - 2) < 64, "copies in flight fit the vmcnt immediate");
+  constexpr int NT = 64 * WAVES * GROUPS;
+  constexpr int QB = 16 * QPW * WAVES;       // query rows per workgroup
+  constexpr int NQF = DP / 32;               // Q fragments (16 bytes each)
+  constexpr int NDB = DP / 16;               // 16-wide head-dim blocks of O^T
+  // LDS tile buffers: STAGES of K and of V per group.
+  constexpr int KBUFS = GROUPS * STAGES;
+  constexpr int VBUFS = GROUPS * STAGES;
+  using MM = Mma16<T>;
+
+  __shared__ __align__(1024) unsigned char k_lds[KBUFS * TILEB];
+  __shared__ __align__(1024) unsigned char v_lds[VBUFS * TILEB];
+  __shared__ __align__(16) int gran[kGranuleWindow];
+
+  // Grid mapping: as paged_prefill_mfma.
+  const int nq = (a.T + QB - 1) / QB;
+  const int wg = (int)blockIdx.x;
+  int h, qr;
+  if ((a.H & 7) == 0) {
+    int j = wg >> 3;
+    if (a.pair_round > 0 && (j / a.pair_round) & 1) {
+      const int lo = j - j % a.pair_round;
+      const int hi = min(lo + a.pair_round, (a.H >> 3) * nq);
+      j = hi - 1 - (j - lo);
+    }
+    h = (wg & 7) + 8 * (j / nq);
+    qr = j % nq;
+  } else {
+    h = wg / nq;
+    qr = wg % nq;
+  }
+  const int qt = nq - 1 - qr;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wall = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = GROUPS == 1 ? 0 : wall / WAVES;  // group of this wavefront
+  const int wave = GROUPS == 1 ? wall : wall % WAVES;  // wavefront within its group
+  const int col = lane & 15, g = lane >> 4;
+  const int qw0 = qt * QB + wave * 16 * QPW;
+  const int kv_end = a.start + min(a.T, (qt + 1) * QB);
+  const int part = (int)blockIdx.y;
+  const int ntiles_all = (kv_end + kTileKeys - 1) / kTileKeys;
+  const int tpp = a.part_keys > 0 ? a.part_keys / kTileKeys : ntiles_all;
+  const int tb = part * tpp;
+  if (tb >= ntiles_all) return;  // uniform: this query tile needs fewer partitions
+  const int key0 = tb * kTileKeys;
+  const bool wave_active = qw0 < a.T;
+  const int wave_first = a.start + qw0;
+  const int wave_last = a.start + min(a.T, qw0 + 16 * QPW) - 1;
+  const int ntiles = min(ntiles_all, tb + tpp) - tb;
+  const int nsteps = (ntiles + GROUPS - 1) / GROUPS;  // loop steps (every group takes them all)
+  const int ntg = (ntiles - grp + GROUPS - 1) / GROUPS;  // tiles of this wave's group
+  int qi[QPW], qpos[QPW];
+#pragma unroll
+  for (int b = 0; b < QPW; ++b) {
+    qi[b] = qw0 + 16 * b + col;
+    qpos[b] = a.start + (qi[b] < a.T ? qi[b] : a.T - 1);
+  }
+
+  // ---- this lane's query fragments (zero past the chunk or past D)
+  uint4 qf[QPW][NQF];
+#pragma unroll
+  for (int b = 0; b < QPW; ++b) {
+    const bool ok = qi[b] < a.T;
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (int64_t)(ok ? qi[b] : 0) * a.q_st + (int64_t)h * a.q_sh;
+#pragma unroll
+    for (int f = 0; f < NQF; ++f) {
+      const int d = 32 * f + 8 * g;
+      qf[b][f] = (ok && d < a.D) ? *reinterpret_cast<const uint4*>(qrow + d) : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // ---- granule window: granules gwin0 .. gwin0 + kGranuleWindow - 1 (gwin0 a
+  // multiple of 4, as every tile's first granule is)
+  const int gshift = a.s_shift - 4;
+  const int gmask = (1 << gshift) - 1;
+  const int sm = a.S - 1;
+  int gwin0 = key0 >> 4;
+  auto fill_window = [&]() {
+    for (int i = tid; i < kGranuleWindow; i += NT) {
+      const int key = (gwin0 + i) << 4;
+      int v = -1;
+      if (key < kv_end) {
+        const int64_t e = load_index(a.bt, a.bt_i64, (int64_t)(key >> a.s_shift) * a.bt_s);
+        if (e >= 0 && e < a.N) v = ((int)e << gshift) + ((key & sm) >> 4);
+      }
+      gran[i] = v;
+    }
+  };
+  fill_window();
+  __syncthreads();
+  // The granules of this group's tile at step u (tile u * GROUPS + grp): lane
+  // j of every four holds granule j. Moves the window first when step u's
+  // tiles leave it, which drains the copies in flight; the condition depends
+  // on u only, so the whole workgroup takes it together.
+  auto tile_granules = [&](int u) -> int {
+    const int s0 = (key0 >> 4) + 4 * GROUPS * u;  // first granule of the step's first tile
+    if (s0 + 4 * GROUPS > gwin0 + kGranuleWindow) {
+      __syncthreads();
+      gwin0 = s0;
+      fill_window();
+      __syncthreads();
+    }
+    return gran[s0 + 4 * grp - gwin0 + (lane & 3)];
+  };
+
+  const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k) + (int64_t)h * a.k_sh * 2;
+  const unsigned char* vbase = reinterpret_cast<const unsigned char*>(a.v) + (int64_t)h * a.v_sh * 2;
+  const uint32_t k_sn2 = (uint32_t)(a.k_sn * 2), v_sn2 = (uint32_t)(a.v_sn * 2);
+  const uint32_t k_ss2 = (uint32_t)(a.k_ss * 2), v_ss2 = (uint32_t)(a.v_ss * 2);
+
+  // Per copy i of this wave: the lane's row within the tile, its source
+  // chunks, and its byte offsets within the granule's K and V rows.
+  auto copy_row = [&](int i) { return (wave * GPW + i) * RPG + lane / CPR; };
+  auto k_chunk = [&](int i) { return (lane % CPR) ^ k_swz<CPR>(copy_row(i)); };
+  auto v_chunk = [&](int i) { return (lane % CPR) ^ v_swz<CPR>(copy_row(i)); };
+  uint32_t koff[GPW], voff[GPW];
+#pragma unroll
+  for (int i = 0; i < GPW; ++i) {
+    koff[i] = (uint32_t)(copy_row(i) & 15) * k_ss2 + (uint32_t)(k_chunk(i) * 16);
+    voff[i] = (uint32_t)(copy_row(i) & 15) * v_ss2 + (uint32_t)(v_chunk(i) * 16);
+  }
+  const bool all_dims = a.D == DP;
+  const int kbuf0 = grp * STAGES, vbuf0 = grp * STAGES;  // this group's first K and V buffers
+  const uint32_t k_lds0 = lds_addr(k_lds) + kbuf0 * TILEB, v_lds0 = lds_addr(v_lds) + vbuf0 * TILEB;
+
+  // The copies of one tile by this wave: per granule j its K and V
+  // sources, whether every row is a key (the scalar-base form), and the
+  // destinations.
+  struct CopyPlan {
+    const unsigned char* kb[GRW];
+    const unsigned char* vb[GRW];
+    int G[GRW];
+    uint32_t kdst, vdst;
+    int kt0;
+    bool fast, live;
+  };
+  // Plans this group's tile of step u (granules gv) into its K buffer KS and
+  // V buffer VS; sets the tile's key mask (bit k: key k has K and V rows).
+  // Nothing is copied past the last tile.
+  auto plan_copies = [&](int u, int gv, int KS, int VS, uint64_t& vm) __attribute__((always_inline)) -> CopyPlan {
+    CopyPlan cp;
+    const int t = u * GROUPS + grp;
+    cp.live = t < ntiles;
+    cp.kt0 = key0 + t * kTileKeys;
+    const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(gv >= 0) & 0xfu;  // granule j valid
+    cp.fast = all_dims && cp.kt0 + kTileKeys <= kv_end && valid == 0xfu;
+    cp.kdst = k_lds0 + KS * TILEB + wave * (GPW * 1024);
+    cp.vdst = v_lds0 + VS * TILEB + wave * (GPW * 1024);
+    const int gw0 = (wave * RW) >> 4;
+#pragma unroll
+    for (int j = 0; j < GRW; ++j) {
+      const int G = __builtin_amdgcn_readlane(gv, gw0 + j);
+      const uint32_t phys = (uint32_t)(G >> gshift), inb = (uint32_t)((G & gmask) << 4);
+      cp.G[j] = G;
+      cp.kb[j] = kbase + (uint64_t)phys * k_sn2 + inb * k_ss2;
+      cp.vb[j] = vbase + (uint64_t)phys * v_sn2 + inb * v_ss2;
+    }
+    vm = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (cp.live && ((valid >> j) & 1u)) vm |= 0xffffull << (16 * j);
+    return cp;
+  };
+  // Issues copy i (one K and one V row group) of a plan.
+  auto copy_one = [&](const CopyPlan& cp, int i) __attribute__((always_inline)) {
+    if (!cp.live) return;
+    const int j = i / CPGW;
+    if (cp.fast) {
+      copy16_to_lds(cp.kb[j], koff[i], cp.kdst + i * 1024);
+      copy16_to_lds(cp.vb[j], voff[i], cp.vdst + i * 1024);
+    } else {
+      const bool ok = cp.G[j] >= 0 && cp.kt0 + copy_row(i) < kv_end;
+      const int ck = k_chunk(i), cv = v_chunk(i);
+      const unsigned char* ks = (ok && ck * 8 < a.D) ? cp.kb[j] + koff[i] : kZeroRow + ck * 16;
+      const unsigned char* vs = (ok && cv * 8 < a.D) ? cp.vb[j] + voff[i] : kZeroRow + cv * 16;
+      copy16_to_lds(ks, cp.kdst + i * 1024);
+      copy16_to_lds(vs, cp.vdst + i * 1024);
+    }
+  };
+  auto copy_all = [&](const CopyPlan& cp) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < GPW; ++i) copy_one(cp, i);
+  };
+
+  f32x4_t oacc[QPW][NDB];
+  float m_run[QPW], l_part[QPW];
+#pragma unroll
+  for (int b = 0; b < QPW; ++b) {
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) oacc[b][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[b] = -INFINITY;
+    l_part[b] = 0.f;
+  }
+
+  // This lane's operand read offsets within its group's stage 0. K: the A
+  // row of key block kb is 32 (kb >> 1) + 4 (kb & 1) + krb, whose swizzle
+  // equals krb's (the added terms leave the bits ks reads alone). V: rows
+  // 32c + 4u + vr at head dims 16db + 4 tr_q, whose swizzle equals vr's.
+  const int krb = 8 * (col >> 2) + (col & 3);
+  int ka[NQF];
+#pragma unroll
+  for (int f = 0; f < NQF; ++f) ka[f] = kbuf0 * TILEB + krb * ROWB + (((4 * f + g) ^ k_swz<CPR>(krb)) << 4);
+  const int tr_j = (lane & 15) >> 2, tr_q = lane & 3;
+  const int vr = 8 * g + tr_j;
+  int va[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    va[db] = vbuf0 * TILEB + vr * ROWB + ((tr_q & 1) << 3) + (((2 * db + (tr_q >> 1)) ^ v_swz<CPR>(vr)) << 4);
+  const float cs = a.scale_log2;
+
+  // QK^T and softmax of the tile in stage ST: packs P for the PV product.
+  auto qk_softmax = [&](int kt0, uint64_t vm, int ST, uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
+    const unsigned char* kl = k_lds + ST * TILEB;
+    // ---- S^T blocks: lane holds keys 32c + 8g + 4hh + i (kb = 2c + hh) of
+    // query column `col` of each 16-row block b. Block kb + 1's K reads go
+    // out before block kb's products; each read feeds QPW products.
+    f32x4_t s[QPW][4];
+    auto read_k = [&](int kb, uint4 (&kv)[NQF]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int f = 0; f < NQF; ++f)
+        kv[f] = *reinterpret_cast<const uint4*>(kl + ka[f] + (32 * (kb >> 1) + 4 * (kb & 1)) * ROWB);
+    };
+    uint4 kv[2][NQF];
+    read_k(0, kv[0]);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      if (kb + 1 < 4) read_k(kb + 1, kv[(kb + 1) & 1]);
+#pragma unroll
+      for (int b = 0; b < QPW; ++b) s[b][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int f = 0; f < NQF; ++f)
+#pragma unroll
+        for (int b = 0; b < QPW; ++b) s[b][kb] = MM::mfma(kv[kb & 1][f], qf[b][f], s[b][kb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- masks (causal, invalid granules), online softmax, P packed for PV
+    const bool full = kt0 + kTileKeys - 1 <= wave_first && vm == ~0ull;
+#pragma unroll
+    for (int b = 0; b < QPW; ++b) {
+      float p[4][4];
+      if (full) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[kb][i] = s[b][kb][i];
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const int k0 = 32 * (kb >> 1) + 8 * g + 4 * (kb & 1);  // within the tile
+          const uint32_t bits = (uint32_t)(vm >> k0) & 0xfu;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = kt0 + k0 + i <= qpos[b] && ((bits >> i) & 1u);
+            p[kb][i] = vis ? s[b][kb][i] : -INFINITY;
+          }
+        }
+      }
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mt = fmaxf(mt, p[kb][i]);
+      mt *= cs;
+      if (__builtin_amdgcn_ballot_w64(mt > m_run[b] + kRescaleSlack) != 0) {
+        mt = cross_group_max(mt);
+        const float m_new = fmaxf(m_run[b], mt);
+        const float alpha = m_run[b] == -INFINITY ? 0.f : fast_exp2(m_run[b] - m_new);
+        m_run[b] = m_new;
+        l_part[b] *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) oacc[b][db] *= alpha;
+      }
+      const float neg_m = m_run[b] == -INFINITY ? 0.f : -m_run[b];
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[kb][i] = fast_exp2(fmaf(p[kb][i], cs, neg_m));
+          ps += p[kb][i];
+        }
+      l_part[b] += ps;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        pb[b][c] = make_uint4(MM::pack2(p[2 * c][0], p[2 * c][1]), MM::pack2(p[2 * c][2], p[2 * c][3]),
+                              MM::pack2(p[2 * c + 1][0], p[2 * c + 1][1]),
+                              MM::pack2(p[2 * c + 1][2], p[2 * c + 1][3]));
+    }
+
+  };
+  // O^T += V^T P^T for the tile in stage ST, per 32-key slice c; each V read
+  // feeds QPW products.
+  auto pv = [&](int ST, const uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
+    const unsigned char* vl = v_lds + ST * TILEB;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      uint4 vv[NDB];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const uint2 lo = TrRead<T>::read(vl + va[db] + (32 * c) * ROWB);
+        const uint2 hi = TrRead<T>::read(vl + va[db] + (32 * c + 4) * ROWB);
+        vv[db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int b = 0; b < QPW; ++b) oacc[b][db] = MM::mfma(vv[db], pb[b][c], oacc[b][db]);
+      __builtin_amdgcn_sched_barrier(0);  // slice 1's V reads wait for slice 0's products
+    }
+  };
+
+  // ---- pipeline, per group: the group's tiles of steps u + 1 .. u + STAGES
+  // - 1 are copied while its tile of step u is computed. At step u: wait for
+  // this wave's copies of its tile (later tiles' copies may stay in flight)
+  // and join the barrier (every wave's copies of it have landed and every
+  // wave is done with the buffers of step u - 1), start the tile of step
+  // u + STAGES - 1 in them, read the granules of the step after it,
+  // compute. Buffers of step u: u % STAGES.
+  auto wait_step = [&](int u) {
+    const int later = ntg - 1 - u;  // this group's tiles after step u whose copies may be in flight
+    if constexpr (STAGES >= 4)
+      if (later >= 2) return wait_and_barrier<4 * GPW>();
+    if constexpr (STAGES >= 3)
+      if (later >= 1) return wait_and_barrier<2 * GPW>();
+    wait_and_barrier<0>();
+  };
+  uint64_t vm[STAGES];
+  int e = tile_granules(0);
+  static_for<0, STAGES - 1>([&](auto sc) {
+    constexpr int SI = decltype(sc)::value;
+    vm[SI] = 0;
+    if (SI < nsteps) {
+      copy_all(plan_copies(SI, e, SI, SI, vm[SI]));
+      if (SI + 1 < nsteps) e = tile_granules(SI + 1);
+    }
+  });
+  for (int u0 = 0; u0 < nsteps; u0 += STAGES) {
+    static_for<0, STAGES>([&](auto sc) {
+      constexpr int SI = decltype(sc)::value;
+      constexpr int SN = (SI + STAGES - 1) % STAGES;  // buffers of step u + STAGES - 1
+      const int u = u0 + SI;
+      if (u >= nsteps) return;
+      wait_step(u);
+      const int un = u + STAGES - 1;
+      if (un < nsteps) {
+        copy_all(plan_copies(un, e, SN, SN, vm[SN]));
+        if (un + 1 < nsteps) e = tile_granules(un + 1);
+      }
+      const int kt0 = key0 + (u * GROUPS + grp) * kTileKeys;
+      if (u < ntg && wave_active && kt0 <= wave_last) {
+        uint4 pb[QPW][2];
+        qk_softmax(kt0, vm[SI], SI, pb);
+        pv(SI, pb);
+      }
+    });
+  }
+
+  // ---- group 1 hands its state to group 0 through the drained tile
+  // buffers: unnormalised outputs in the K buffers, (max, partial sum) in the
+  // V buffers, lane-major so the writes and reads are conflict-free.
+  if constexpr (GROUPS == 2) {
+    constexpr int OITEMS = QPW * 4 * NDB;  // output floats per lane
+    static_assert(OITEMS * 64 * WAVES * 4 <= KBUFS * TILEB, "group 1's outputs fit the K buffers");
+    static_assert(2 * QPW * 64 * WAVES * 4 <= VBUFS * TILEB, "group 1's (max, sum) fit the V buffers");
+    float* xo = reinterpret_cast<float*>(k_lds) + wave * (OITEMS * 64) + lane;
+    float* xm = reinterpret_cast<float*>(v_lds) + wave * (2 * QPW * 64) + lane;
+    wait_and_barrier<0>();  // every wave is done with the tile buffers
+    if (grp == 1) {
+#pragma unroll
+      for (int b = 0; b < QPW; ++b) {
+        xm[(2 * b) * 64] = m_run[b];
+        xm[(2 * b + 1) * 64] = l_part[b];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xo[((b * NDB + db) * 4 + i) * 64] = oacc[b][db][i];
+      }
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int b = 0; b < QPW; ++b) {
+      const float m1 = xm[(2 * b) * 64], l1 = xm[(2 * b + 1) * 64];
+      const float m_new = fmaxf(m_run[b], m1);
+      const float a0 = m_run[b] == -INFINITY ? 0.f : fast_exp2(m_run[b] - m_new);
+      const float a1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - m_new);
+      m_run[b] = m_new;
+      l_part[b] = l_part[b] * a0 + l1 * a1;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          oacc[b][db][i] = oacc[b][db][i] * a0 + xo[((b * NDB + db) * 4 + i) * 64] * a1;
+    }
+  }
+
+  // ---- normalise and store (as paged_prefill_mfma)
+#pragma unroll
+  for (int b = 0; b < QPW; ++b) {
+    const float l = cross_group_sum(l_part[b]);
+    if (qi[b] >= a.T) continue;
+    if (a.part_keys > 0) {
+      const int np = (a.start + qi[b] + a.part_keys) / a.part_keys;
+      if (part >= np) continue;
+      if (np > 1) {
+        const size_t slot = ((size_t)qi[b] * a.H + h) * a.max_parts + part;
+        if (g == 0) a.ws_ml[slot] = make_float2(m_run[b], l);
+        float* wa = a.ws_acc + slot * a.D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const int d0 = 16 * db + 4 * g;
+          if (d0 >= a.D) continue;
+          *reinterpret_cast<float4*>(wa + d0) =
+              make_float4(oacc[b][db][0], oacc[b][db][1], oacc[b][db][2], oacc[b][db][3]);
+        }
+        continue;
+      }
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    T* orow = reinterpret_cast<T*>(a.out) + (int64_t)qi[b] * a.o_st + (int64_t)h * a.o_sh;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int d0 = 16 * db + 4 * g;
+      if (d0 >= a.D) continue;
+      uint2 w;
+      w.x = MM::pack2(oacc[b][db][0] * inv, oacc[b][db][1] * inv);
+      w.y = MM::pack2(oacc[b][db][2] * inv, oacc[b][db][3] * inv);
+      *reinterpret_cast<uint2*>(orow + d0) = w;
+    }
+  }
+}
+
 // Workgroups of kernel `fn` (threads each) resident per CU at once.
 static int resident_per_cu(const void* fn, int threads) {
   int n = 0;
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) == hipSuccess ? n : 0;
 }
 
+// Whether paged_prefill_tr takes this call: power-of-two blocks of at least
+// 16 keys, D a multiple of 8, 16-byte aligned rows, and the 32-bit offsets it
+// forms in range (granule indices, block strides, in-block row offsets).
+static bool tr_eligible(const PrefillArgs& a) {
+  if (a.s_shift < 4 || a.D % 8 != 0) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  if ((a.N << (a.s_shift - 4)) >= lim) return false;
+  for (int64_t sn : {a.k_sn, a.v_sn})
+    if (sn < 0 || sn * 2 >= ((int64_t)1 << 32)) return false;
+  for (int64_t ss : {a.k_ss, a.v_ss})
+    if (ss < 0 || (int64_t)a.S * ss * 2 >= lim || (ss * 2) % 16 != 0) return false;
+  for (int64_t sx : {a.k_sn, a.v_sn, a.k_sh, a.v_sh})
+    if ((sx * 2) % 16 != 0) return false;
+  return (reinterpret_cast<uintptr_t>(a.k) % 16) == 0 && (reinterpret_cast<uintptr_t>(a.v) % 16) == 0;
+}
+
+template <typename T, int DP, int WAVES, int QPW, int STAGES, int GROUPS>
+hipError_t launch_tr_cfg(const PrefillArgs& a, hipStream_t stream) {
+  constexpr int QB = 16 * QPW * WAVES;
+  constexpr int NT = 64 * WAVES * GROUPS;
+  const int64_t wgs = ((int64_t)a.T + QB - 1) / QB * a.H;
+  const void* fn = reinterpret_cast<const void*>(&paged_prefill_tr<T, DP, WAVES, QPW, STAGES, GROUPS>);
+  static const int per_cu = resident_per_cu(fn, NT);
+  PrefillArgs b = a;
+  const bool split = a.part_keys > 0;
+  b.pair_round = (!split && per_cu == 2 && (a.H & 7) == 0 && a.cus % 8 == 0 && wgs > a.cus &&
+                  wgs <= 2 * a.cus)
+                     ? a.cus / 8 : 0;
+  const dim3 grid((unsigned)wgs, split ? (unsigned)a.max_parts : 1u);
+  hipLaunchKernelGGL((paged_prefill_tr<T, DP, WAVES, QPW, STAGES, GROUPS>), grid, dim3(NT), 0, stream, b);
+  return hipGetLastError();
+}
+
+// MINIVLLM_HIP_PREFILL_TR (read on every call) overrides the choice below for
+// tuning and tests: 0 takes paged_prefill_mfma; otherwise its decimal digits
+// set paged_prefill_tr's groups minus one (thousands), wavefronts per group,
+// 16-row query blocks per wavefront and tiles in flight per group (412, 422,
+// 812, 1412 or 1422). -1: unset.
+int prefill_tr_mode() {
+  const char* e = std::getenv("MINIVLLM_HIP_PREFILL_TR");
+  return e && *e ? std::atoi(e) : -1;
+}
+
+// paged_prefill_tr configuration for a call, measured on MI355X (bf16,
+// D = 128, S = 16, 16 heads unless noted):
+//   * 1422 (two groups of four 32-row wavefronts per 128-row query tile,
+//     one workgroup per CU): chunks after a prefix at least as long whose
+//     128-row tiles fill the CUs (2048 rows after 2048: 80 us; 412: 87);
+//   * 1412 (two groups of four 16-row wavefronts per 64-row tile): grids of
+//     64-row tiles that leave CUs empty, where splitting each workgroup's keys
+//     over two groups halves its serial chain (512 rows at 0: 13.5 us; 412:
+//     14.5);
+//   * 412 (two workgroups of four 16-row wavefronts per CU) otherwise, and
+//     whenever the keys are split over workgroups (its cost model assumes
+//     64-row tiles).
+int prefill_tr_choice(const PrefillArgs& a) {
+  const int forced = prefill_tr_mode();
+  if (forced >= 0) return forced;
+  const int64_t wgs128 = ((int64_t)a.T + 127) / 128 * a.H, wgs64 = ((int64_t)a.T + 63) / 64 * a.H;
+  if (a.part_keys > 0) return 412;
+  if (a.start >= a.T && wgs128 >= a.cus) return 1422;
+  if (wgs64 <= a.cus) return 1412;
+  return 412;
+}
+
+template <typename T, int DP>
+hipError_t launch_tr(const PrefillArgs& a, int mode, hipStream_t stream) {
+  switch (mode) {
+    case 422: return launch_tr_cfg<T, DP, 4, 2, 2, 1>(a, stream);
+    case 812: return launch_tr_cfg<T, DP, 8, 1, 2, 1>(a, stream);
+    case 1412: return launch_tr_cfg<T, DP, 4, 1, 2, 2>(a, stream);
+    case 1422: return launch_tr_cfg<T, DP, 4, 2, 2, 2>(a, stream);
+    default: return launch_tr_cfg<T, DP, 4, 1, 2, 1>(a, stream);  // 412
+  }
+}
+
 template <typename T, int DP, int WAVES>
 hipError_t launch_waves(const PrefillArgs& a, hipStream_t stream) {
+  if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128) && WAVES == 4) {
+    if (tr_eligible(a)) {
+      const int mode = prefill_tr_choice(a);
+      if (mode != 0) return launch_tr<T, DP>(a, mode, stream);
+    }
+  }
   constexpr int QB = 16 * WAVES;
   const void* fn = reinterpret_cast<const void*>(&paged_prefill_mfma<T, DP, WAVES, 1>);
   static const int per_cu = resident_per_cu(fn, 64 * WAVES);

@@ -133,6 +133,73 @@ def test_forced_key_split_matches_oracle(monkeypatch, start, T, H, D, S, keys, d
     check(out, q, pool, table, start, layer)
 
 
+# Every configuration of the matrix-core prefill, selected through
+# MINIVLLM_HIP_PREFILL_TR: 0 is paged_prefill_mfma; the others are
+# paged_prefill_tr's (groups - 1, wavefronts per group, 16-row blocks per
+# wavefront, tiles in flight). Cases: block sizes 16 .. 256 (one to sixteen
+# 16-key granules per block), head dims 64 and 128, partial tiles, and
+# contexts past 16384 keys, where the workgroup's block-table window moves.
+TR_CONFIGS = ["0", "412", "422", "812", "1412", "1422"]
+TR_CASES = [
+    # start, T, H, D, S
+    (0, 406, 8, 128, 16),
+    (1000, 200, 4, 128, 16),
+    (63, 65, 4, 128, 32),
+    (100, 130, 4, 64, 64),
+    (5, 300, 2, 128, 256),
+    (16200, 300, 2, 128, 16),
+    (16300, 200, 1, 64, 16),
+]
+_TR_EXPECTED: dict = {}
+
+
+def _tr_case(start, T, H, D, S, dtype):
+    key = (start, T, H, D, S, dtype)
+    if key not in _TR_EXPECTED:
+        qkv, pool, table, layer = prefill_case(start, T, H, D, S, dtype, seed=23)
+        q = qkv.to(DEV)[:, 0]
+        want = ora.paged_prefill(fx.to_numpy(q), fx.to_numpy(pool.k), fx.to_numpy(pool.v),
+                                 table.numpy(), start, layer)
+        _TR_EXPECTED.clear()  # one case's pools at a time
+        _TR_EXPECTED[key] = (q, pool, table, layer, want)
+    return _TR_EXPECTED[key]
+
+
+@pytest.mark.parametrize("config", TR_CONFIGS)
+@pytest.mark.parametrize("start,T,H,D,S", TR_CASES)
+def test_prefill_kernel_configs_match_oracle(monkeypatch, start, T, H, D, S, config):
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_TR", config)
+    q, pool, table, layer, want = _tr_case(start, T, H, D, S, torch.bfloat16)
+    print(f"  config {config}", flush=True)
+    got = run_hip(q, pool, table, start, layer).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, **BF16_TOL)
+
+
+@pytest.mark.parametrize("config", TR_CONFIGS[1:])
+@pytest.mark.parametrize("split_keys", ["0", "128"], ids=["whole", "split128"])
+def test_prefill_kernel_configs_f16_masked_and_split(monkeypatch, config, split_keys):
+    """Each paged_prefill_tr configuration in f16, with invalid table entries
+    (masked keys, a row with none visible) and with its keys split over
+    workgroups."""
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_TR", config)
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_SPLIT_KEYS", split_keys)
+    start, T, H, D, S = 200, 180, 4, 128, 16
+    qkv, pool, table, layer = prefill_case(start, T, H, D, S, torch.float16, seed=29)
+    q = qkv.to(DEV)[:, 0]
+    bad = table.clone()
+    bad[3] = -1
+    bad[15] = pool.num_blocks + 1
+    print(f"  config {config} split {split_keys}", flush=True)
+    out = run_hip(q, pool, bad, start, layer)
+    check(out, q, pool, bad, start, layer)
+    first = table.clone()
+    first[0] = -1
+    out0 = run_hip(q[:40], pool, first, 0, layer)
+    check(out0, q[:40], pool, first, 0, layer)
+    assert torch.count_nonzero(out0[:16]) == 0
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_key_split_agrees_with_unsplit(monkeypatch, dtype):
     """The automatic split (a small chunk after a long prefix) against the
