@@ -1,9 +1,14 @@
-"""In-tree build of libminivllm_hip.so (HIP C++ for gfx950).
+"""In-tree build of libminivllm_hip.so (HIP C++ for gfx950) and its PyTorch
+binding.
 
 Every ``csrc/*.hip`` source is compiled with hipcc into an object under
 ``mini-gpt-inference_amd/_build/`` (in parallel), then linked into
 ``minivllm/_native/libminivllm_hip.so``. The library exports the C ABI
 declared in ``include/minivllm_hip.h``.
+
+``csrc/torch_ops.cpp`` (host C++, no device code) is then compiled with the
+host compiler against PyTorch's headers into the extension module
+``minivllm/_native/_hip_ops<ext>``, which links the library by ``$ORIGIN``.
 
 Packed-FP32 instructions are disabled on the device pass
 (``-target-feature -packed-fp32-ops``); hipcc's host pass warns that it does
@@ -43,6 +48,12 @@ MFMA_SOURCES = {"paged_prefill.hip"}
 
 def library_path() -> Path:
     return LIB_DIR / LIB_NAME
+
+
+def ops_path() -> Path:
+    import sysconfig
+
+    return LIB_DIR / ("_hip_ops" + sysconfig.get_config_var("EXT_SUFFIX"))
 
 
 def _hipcc() -> str:
@@ -93,6 +104,34 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = out.with_name(out.name + f".tmp{os.getpid()}")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)],
          verbose)
+    os.replace(tmp, out)
+    build_torch_ops(verbose)
+    return out
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """Compiles csrc/torch_ops.cpp into the _hip_ops extension module (needs
+    libminivllm_hip.so in place: it links against it)."""
+    import sysconfig
+
+    import torch
+
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if not cxx:
+        raise RuntimeError("no host C++ compiler (g++) for the PyTorch binding")
+    tdir = Path(torch.__file__).resolve().parent
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    out = ops_path()
+    tmp = out.with_name(out.name + f".tmp{os.getpid()}")
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared",
+          "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=_hip_ops",
+          "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+          f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+          f"-I{sysconfig.get_paths()['include']}", f"-I{rocm / 'include'}", f"-I{INCLUDE}",
+          str(CSRC / "torch_ops.cpp"), "-o", str(tmp),
+          f"-L{tdir / 'lib'}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+          f"-L{LIB_DIR}", "-lminivllm_hip", "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(tmp, out)
     return out
 

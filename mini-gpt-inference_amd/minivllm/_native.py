@@ -12,7 +12,7 @@ import threading
 
 import torch
 
-from ._build import library_path
+from ._build import library_path, ops_path
 
 MGI_OK = 0
 MGI_EINVAL = -1
@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_ops = None
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -117,6 +118,33 @@ def lib() -> ctypes.CDLL:
             _declare(handle)
             _lib = handle
     return _lib
+
+
+def ops():
+    """The PyTorch binding (_hip_ops: kv_append, paged_decode, paged_prefill
+    on tensors, validated in C++, calling the C ABI on the current stream).
+    Raises RuntimeError when it is unavailable."""
+    global _ops
+    if _ops is not None:
+        return _ops
+    lib()  # the library first: a clear error when it is the missing piece
+    with _lock:
+        if _ops is None:
+            import importlib.util
+
+            path = ops_path()
+            if not path.exists():
+                raise RuntimeError(
+                    f"HIP extension not built: {path} is missing "
+                    "(run `python -c 'import __graft_entry__ as g; g.build()'` at the repo root)")
+            try:
+                spec = importlib.util.spec_from_file_location("minivllm._hip_ops", path)
+                mod = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(mod)
+            except (ImportError, OSError) as exc:
+                raise RuntimeError(f"HIP extension failed to load: {exc}") from exc
+            _ops = mod
+    return _ops
 
 
 @functools.lru_cache(maxsize=1024)

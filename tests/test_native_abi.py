@@ -32,6 +32,27 @@ def test_library_exports_every_declared_symbol():
     assert lib.mgi_abi_version() == 103
 
 
+def test_torch_binding_loads_and_validates_on_the_host():
+    """The _hip_ops extension (csrc/torch_ops.cpp) loads next to the library
+    and raises the wrappers' ValueErrors before any device work: CPU tensors
+    are refused first."""
+    ops = _native.ops()
+    for name in ("kv_append", "paged_decode", "paged_prefill"):
+        assert callable(getattr(ops, name)), name
+    from minivllm import hip_paged_decode as hpd
+    from minivllm.kv_block_pool import KVBlockPool
+
+    pool = KVBlockPool(1, 4, 16, 2, 64)
+    q = torch.zeros(1, 2, 64)
+    with pytest.raises(ValueError, match="q must be on a GPU device"):
+        hpd.paged_attention_batch_hip(q, pool, torch.zeros(1, 1, dtype=torch.long),
+                                      torch.ones(1, dtype=torch.long), 0)
+    with pytest.raises(ValueError, match="KV pool must be on a GPU device"):
+        hpd.kv_append(pool, 0, q, q, torch.zeros(1, dtype=torch.long))
+    with pytest.raises(ValueError, match="q must be on a GPU device"):
+        hpd.paged_prefill_hip(q, pool, torch.zeros(1, dtype=torch.long), 0, 0)
+
+
 def test_split_tokens_and_workspace_sizes():
     lib = _native.lib()
     # decode microbench shape: M = 256 columns of S = 16 -> 8 partitions of 512
