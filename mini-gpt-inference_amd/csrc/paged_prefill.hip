@@ -783,7 +783,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       fill_window();
       __syncthreads();
     }
-    return gran[s0 + 4 * grp - gwin0 + (lane & 3)];
+    return gran[s0 - gwin0 + (lane & (4 * GROUPS - 1))];
   };
 
   const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k) + (int64_t)h * a.k_sh * 2;
@@ -817,19 +817,19 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
     int kt0;
     bool fast, live;
   };
-  // Plans this group's tile of step u (granules gv) into its K buffer KS and
-  // V buffer VS; sets the tile's key mask (bit k: key k has K and V rows).
-  // Nothing is copied past the last tile.
-  auto plan_copies = [&](int u, int gv, int KS, int VS, uint64_t& vm) __attribute__((always_inline)) -> CopyPlan {
+  // Plans group tg's tile of step u (granules gv) into that group's K buffer
+  // KS and V buffer VS; sets the tile's key mask (bit k: key k has K and V
+  // rows). Nothing is copied past the last tile.
+  auto plan_copies = [&](int u, int gv, int KS, int VS, uint64_t& vm, int tg) __attribute__((always_inline)) -> CopyPlan {
     CopyPlan cp;
-    const int t = u * GROUPS + grp;
+    const int t = u * GROUPS + tg;
     cp.live = t < ntiles;
     cp.kt0 = key0 + t * kTileKeys;
-    const uint32_t valid = (uint32_t)__builtin_amdgcn_ballot_w64(gv >= 0) & 0xfu;  // granule j valid
+    const uint32_t valid = ((uint32_t)__builtin_amdgcn_ballot_w64(gv >= 0) >> (4 * tg)) & 0xfu;  // granule j valid
     cp.fast = all_dims && cp.kt0 + kTileKeys <= kv_end && valid == 0xfu;
-    cp.kdst = k_lds0 + KS * TILEB + wave * (GPW * 1024);
-    cp.vdst = v_lds0 + VS * TILEB + wave * (GPW * 1024);
-    const int gw0 = (wave * RW) >> 4;
+    cp.kdst = lds_addr(k_lds) + (tg * STAGES + KS) * TILEB + wave * (GPW * 1024);
+    cp.vdst = lds_addr(v_lds) + (tg * STAGES + VS) * TILEB + wave * (GPW * 1024);
+    const int gw0 = 4 * tg + ((wave * RW) >> 4);
 #pragma unroll
     for (int j = 0; j < GRW; ++j) {
       const int G = __builtin_amdgcn_readlane(gv, gw0 + j);
@@ -1008,13 +1008,29 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       if (later >= 1) return wait_and_barrier<2 * GPW>();
     wait_and_barrier<0>();
   };
+  // The copies of step u into buffers ST: with two groups, group 0 copies
+  // both groups' tiles and group 1 only derives its tile's mask, so group 1
+  // starts computing right after the barrier while group 0 issues.
+  auto issue_step = [&](int u, int gv, int ST, uint64_t& vm_own) __attribute__((always_inline)) {
+    if constexpr (GROUPS == 1) {
+      copy_all(plan_copies(u, gv, ST, ST, vm_own, 0));
+    } else {
+      uint64_t vm_other;
+      if (grp == 0) {
+        copy_all(plan_copies(u, gv, ST, ST, vm_own, 0));
+        copy_all(plan_copies(u, gv, ST, ST, vm_other, 1));
+      } else {
+        (void)plan_copies(u, gv, ST, ST, vm_own, 1);
+      }
+    }
+  };
   uint64_t vm[STAGES];
   int e = tile_granules(0);
   static_for<0, STAGES - 1>([&](auto sc) {
     constexpr int SI = decltype(sc)::value;
     vm[SI] = 0;
     if (SI < nsteps) {
-      copy_all(plan_copies(SI, e, SI, SI, vm[SI]));
+      issue_step(SI, e, SI, vm[SI]);
       if (SI + 1 < nsteps) e = tile_granules(SI + 1);
     }
   });
@@ -1027,7 +1043,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       wait_step(u);
       const int un = u + STAGES - 1;
       if (un < nsteps) {
-        copy_all(plan_copies(un, e, SN, SN, vm[SN]));
+        issue_step(un, e, SN, vm[SN]);
         if (un + 1 < nsteps) e = tile_granules(un + 1);
       }
       const int kt0 = key0 + (u * GROUPS + grp) * kTileKeys;
