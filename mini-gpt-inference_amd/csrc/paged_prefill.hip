@@ -555,22 +555,24 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
 
 // ------------------------------------------------------------------------
 // Direct-to-LDS variant (2-byte types, head dims 64 and 128, power-of-two
-// block sizes of at least 16). Same work split, grid mapping, numerics and
-// outputs as paged_prefill_mfma; what changes is how key tiles reach the
-// matrix cores and how little per-tile work the wavefronts spend on it:
+// block sizes of at least 16). Same grid mapping, numerics and outputs as
+// paged_prefill_mfma; what changes is how key tiles reach the matrix cores
+// and how little per-tile work the wavefronts spend on it:
 //   * A key tile is 64 keys = four 16-key granules, and a granule lies in one
 //     pool block (S is a power of two >= 16). The workgroup keeps a window of
 //     the block table in LDS as one int per granule: G = block * (S / 16) +
 //     (offset in block) / 16, or -1 where the table entry is invalid or the
-//     granule starts past the chunk. One 16-byte LDS read yields a tile's
-//     four granules; what follows from them is wave-uniform scalar work.
+//     granule starts past the chunk. One LDS read per step gives lanes
+//     0 .. 4 GROUPS - 1 the step's granules; what follows from them is
+//     wave-uniform scalar work.
 //   * K and V tiles are copied from HBM straight into LDS by 16-byte
 //     global_load_lds copies (one instruction moves 1 KiB: RPG whole key
-//     rows); each wavefront copies whole granules. When a tile's granules are
-//     all valid and inside the chunk, a copy is the granule's base address in
-//     scalar registers plus a per-lane 32-bit offset fixed for the whole
-//     loop. Otherwise each lane picks its source row, and keys past the
-//     chunk, invalid granules and head dims past D read a zero row.
+//     rows); each copying wavefront takes a contiguous run of a tile's rows.
+//     When a tile's granules are all valid and inside the chunk, a copy is
+//     the granule's base address in scalar registers plus a per-lane 32-bit
+//     offset fixed for the whole loop. Otherwise each lane picks its source
+//     row, and keys past the chunk, invalid granules and head dims past D
+//     read a zero row.
 //   * Rows store their 16-byte chunk c at c ^ ks(r) (K) and c ^ vs(r) (V),
 //     swizzles chosen by measuring these kernels' read sequences on MI355X:
 //     ks(r) = (r & 3) | ((r >> 1) & (CPR - 4)); vs(r) = 2 (r & 3) |
@@ -586,11 +588,11 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
 //     j = 0..3 (the instruction's lane layout, measured on MI355X), so lanes
 //     addressing V rows (keys) 8g + 4u + j at head dims 16db + 4q give lane i
 //     head dim 16db + i of four consecutive keys.
-//   * Two stages: tile t + 1 is copied while tile t is computed, with one
-//     barrier per tile. The loop body exists once per stage, so the LDS
-//     offsets of the operand reads are immediates. The copies are inline
-//     assembly, so the compiler adds no waits of its own for them; the loop
-//     waits for them explicitly (each wave's copies, then the barrier).
+//   * STAGES tiles in flight (per group), one barrier per step. The loop body
+//     exists once per stage, so the LDS offsets of the operand reads are
+//     immediates. The copies are inline assembly, so the compiler adds no
+//     waits of its own for them; the loop waits for them explicitly (each
+//     wave's copies, then the barrier).
 template <int CPR>
 __device__ __forceinline__ int k_swz(int row) {
   return (row & 3) | ((row >> 1) & (CPR - 4));
@@ -660,10 +662,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // GROUPS = 2 splits the workgroup's wavefronts into two groups of WAVES that
-// cover the same query rows: group r takes the key tiles t with t % 2 == r,
-// each through its own STAGES tile buffers, and at the end group 1 hands its
-// softmax state (running max, partial sums, unnormalised output) to group 0
-// through LDS, which merges and stores. A wavefront can then own 32 query rows
+// cover the same query rows: group r computes the key tiles t with
+// t % 2 == r, each through its own STAGES tile buffers, and at the end group
+// 1 hands its softmax state (running max, partial sums, unnormalised output)
+// to group 0 through LDS, which merges and stores. Group 0's wavefronts issue
+// the copies of both groups' tiles. A wavefront can then own 32 query rows
 // (each K and V read from LDS feeds two products) while two wavefronts share
 // every SIMD.
 template <typename T, int DP, int WAVES, int QPW, int STAGES, int GROUPS>
@@ -681,7 +684,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   constexpr int RW = GPW * RPG;              // tile rows per wave
   constexpr int GRW = RW >= 16 ? RW / 16 : 1;  // granules a wave's rows lie in
   constexpr int CPGW = GPW / GRW;            // copies per such granule
-  static_assert(2 * GPW * (STAGES - 2) < 64, "copies in flight fit the vmcnt immediate");
+  static_assert(2 * GPW * GROUPS * (STAGES - 2) < 64, "copies in flight fit the vmcnt immediate");
   constexpr int NT = 64 * WAVES * GROUPS;
   constexpr int QB = 16 * QPW * WAVES;       // query rows per workgroup
   constexpr int NQF = DP / 32;               // Q fragments (16 bytes each)
@@ -804,7 +807,6 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   }
   const bool all_dims = a.D == DP;
   const int kbuf0 = grp * STAGES, vbuf0 = grp * STAGES;  // this group's first K and V buffers
-  const uint32_t k_lds0 = lds_addr(k_lds) + kbuf0 * TILEB, v_lds0 = lds_addr(v_lds) + vbuf0 * TILEB;
 
   // The copies of one tile by this wave: per granule j its K and V
   // sources, whether every row is a key (the scalar-base form), and the
@@ -970,7 +972,6 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
                               MM::pack2(p[2 * c + 1][0], p[2 * c + 1][1]),
                               MM::pack2(p[2 * c + 1][2], p[2 * c + 1][3]));
     }
-
   };
   // O^T += V^T P^T for the tile in stage ST, per 32-key slice c; each V read
   // feeds QPW products.
@@ -995,17 +996,18 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
 
   // ---- pipeline, per group: the group's tiles of steps u + 1 .. u + STAGES
   // - 1 are copied while its tile of step u is computed. At step u: wait for
-  // this wave's copies of its tile (later tiles' copies may stay in flight)
-  // and join the barrier (every wave's copies of it have landed and every
+  // this wave's copies of its tile (later tiles' copies, 2 GPW per group
+  // tile, may stay in flight; group 0 issues them for both groups, group 1
+  // has none) and join the barrier (every wave's copies of it have landed and every
   // wave is done with the buffers of step u - 1), start the tile of step
   // u + STAGES - 1 in them, read the granules of the step after it,
   // compute. Buffers of step u: u % STAGES.
   auto wait_step = [&](int u) {
     const int later = ntg - 1 - u;  // this group's tiles after step u whose copies may be in flight
     if constexpr (STAGES >= 4)
-      if (later >= 2) return wait_and_barrier<4 * GPW>();
+      if (later >= 2) return wait_and_barrier<4 * GPW * GROUPS>();
     if constexpr (STAGES >= 3)
-      if (later >= 1) return wait_and_barrier<2 * GPW>();
+      if (later >= 1) return wait_and_barrier<2 * GPW * GROUPS>();
     wait_and_barrier<0>();
   };
   // The copies of step u into buffers ST: with two groups, group 0 copies
