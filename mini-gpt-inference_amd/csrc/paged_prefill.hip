@@ -1185,7 +1185,12 @@ int prefill_tr_mode() {
 // D = 128, S = 16, 16 heads unless noted):
 //   * 1422 (two groups of four 32-row wavefronts per 128-row query tile,
 //     one workgroup per CU): chunks after a prefix at least as long whose
-//     128-row tiles fill the CUs (2048 rows after 2048: 80 us; 412: 87);
+//     128-row tiles fill the CUs (2048 rows after 2048: 72-80 us; 412:
+//     77-87), and chunks whose 128-row tiles take more than one round of the
+//     CUs while the mean tile attends to at least 20 key tiles (4096 rows at
+//     0: 85 us, 412: 94; 2560 rows: 48 / 52.5; 8192 rows: 296 / 348; 3072
+//     after 1024: 85 / 90). Below 20 the two groups' hand-over and the
+//     one-per-CU grid lose (1024 rows at 0 with 64 heads: 46.6 / 43.3);
 //   * 1412 (two groups of four 16-row wavefronts per 64-row tile): grids of
 //     64-row tiles that leave CUs empty, where splitting each workgroup's keys
 //     over two groups halves its serial chain (512 rows at 0: 13.5 us; 412:
@@ -1198,7 +1203,8 @@ int prefill_tr_choice(const PrefillArgs& a) {
   if (forced >= 0) return forced;
   const int64_t wgs128 = ((int64_t)a.T + 127) / 128 * a.H, wgs64 = ((int64_t)a.T + 63) / 64 * a.H;
   if (a.part_keys > 0) return 412;
-  if (a.start >= a.T && wgs128 >= a.cus) return 1422;
+  const int64_t mean_keys = (int64_t)a.start + a.T / 2;  // keys the mean query tile attends to
+  if (wgs128 >= a.cus && (a.start >= a.T || (wgs128 > a.cus && mean_keys >= 20 * kTileKeys))) return 1422;
   if (wgs64 <= a.cus) return 1412;
   return 412;
 }
