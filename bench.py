@@ -603,8 +603,9 @@ def e2e_c1_speedup(dev):
 
 def cpu_threads() -> tuple[int, int]:
     """Threads of the CPU baseline: every core of this process's affinity set,
-    capped by OMP_NUM_THREADS when the environment sets it (the host share a
-    GPU box allots to its one GPU). Returns (threads used, affinity cores)."""
+    capped by OMP_NUM_THREADS when the environment sets it (the host's share
+    of cores for its one GPU on a shared machine). Returns (threads used,
+    affinity cores)."""
     aff = len(os.sched_getaffinity(0))
     share = int(os.environ.get("OMP_NUM_THREADS") or 0)
     return (min(aff, share) if share > 0 else aff), aff
