@@ -275,6 +275,29 @@ def test_balanced_split_with_empty_and_one_token_contexts(B, tiers, monkeypatch)
     assert (got[ctx.numpy() == 0] == 0).all()
 
 
+@pytest.mark.parametrize("B", [4096, 4100])
+def test_largest_balanced_batch_and_the_partition_fallback(B):
+    """The balanced split holds the batch's block prefix sums in LDS, 4096
+    sequences at most (64 per lane of its scan); one more row takes the
+    partition split. Both against the C oracle. At this batch the library
+    splits only tables wider than one 2048-token partition, so the table
+    has 130 blocks and a few contexts fill it."""
+    S, H, D, M = 16, 4, 64, 130
+    g = torch.Generator().manual_seed(B)
+    choices = torch.tensor([0, 1, 15, 16, 17, 40, 200, M * S])
+    ctx = choices[torch.randint(len(choices), (B,), generator=g)]
+    N = int(((ctx + S - 1) // S).sum()) + 8
+    q, pool, tables, lens, layer = _small_case(B, H, D, S, ctx.tolist(), torch.float32, seed=B, N=N)
+    tables = torch.nn.functional.pad(tables, (0, M - tables.shape[1]), value=-1)
+    waves = hpd._native.lib().mgi_paged_decode_balanced_waves(B, H, D, S, M, 0)
+    assert (waves > 0) == (B <= 4096), waves
+    print(f"  B={B} balanced waves per head group {waves}", flush=True)
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
+    want = c_oracle.paged_decode(*oracle_args(q, pool, tables, lens, layer))
+    np.testing.assert_allclose(got, want, **F32_TOL)
+    assert (got[ctx.numpy() == 0] == 0).all()
+
+
 @pytest.mark.parametrize("tiers", [None, (1, 16)])
 def test_balanced_split_ignores_stale_workspace(tiers, monkeypatch):
     """The workspace is used as found: NaN bytes, zeros, or ticket counters
