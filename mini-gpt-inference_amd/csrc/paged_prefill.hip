@@ -867,15 +867,21 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
     for (int i = 0; i < GPW; ++i) copy_one(cp, i);
   };
 
-  f32x4_t oacc[QPW][NDB];
-  float m_run[QPW], l_part[QPW];
+  // Running sums of P come out of the PV products: lacc[b] = ones^T P^T, a
+  // 16-row block of ones in place of V^T, so each lane holds the sum over
+  // every key of its query column, four times (no VALU adds, no cross-lane
+  // sum at the end). The sum is of the 2-byte P the output accumulates.
+  f32x4_t oacc[QPW][NDB], lacc[QPW];
+  float m_run[QPW];
 #pragma unroll
   for (int b = 0; b < QPW; ++b) {
 #pragma unroll
     for (int i = 0; i < NDB; ++i) oacc[b][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    lacc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m_run[b] = -INFINITY;
-    l_part[b] = 0.f;
   }
+  const uint32_t one2 = MM::pack2(1.f, 1.f);
+  const uint4 ones = make_uint4(one2, one2, one2, one2);
 
   // This lane's operand read offsets within its group's stage 0. K: the A
   // row of key block kb is 32 (kb >> 1) + 4 (kb & 1) + krb, whose swizzle
@@ -952,20 +958,15 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
         const float m_new = fmaxf(m_run[b], mt);
         const float alpha = m_run[b] == -INFINITY ? 0.f : fast_exp2(m_run[b] - m_new);
         m_run[b] = m_new;
-        l_part[b] *= alpha;
+        lacc[b] *= alpha;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) oacc[b][db] *= alpha;
       }
       const float neg_m = m_run[b] == -INFINITY ? 0.f : -m_run[b];
-      float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[kb][i] = fast_exp2(fmaf(p[kb][i], cs, neg_m));
-          ps += p[kb][i];
-        }
-      l_part[b] += ps;
+        for (int i = 0; i < 4; ++i) p[kb][i] = fast_exp2(fmaf(p[kb][i], cs, neg_m));
 #pragma unroll
       for (int c = 0; c < 2; ++c)
         pb[b][c] = make_uint4(MM::pack2(p[2 * c][0], p[2 * c][1]), MM::pack2(p[2 * c][2], p[2 * c][3]),
@@ -973,8 +974,8 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
                               MM::pack2(p[2 * c + 1][2], p[2 * c + 1][3]));
     }
   };
-  // O^T += V^T P^T for the tile in stage ST, per 32-key slice c; each V read
-  // feeds QPW products.
+  // O^T += V^T P^T (and the row sums) for the tile in stage ST, per 32-key
+  // slice c; each V read feeds QPW products.
   auto pv = [&](int ST, const uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
     const unsigned char* vl = v_lds + ST * TILEB;
 #pragma unroll
@@ -990,6 +991,8 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int b = 0; b < QPW; ++b) oacc[b][db] = MM::mfma(vv[db], pb[b][c], oacc[b][db]);
+#pragma unroll
+      for (int b = 0; b < QPW; ++b) lacc[b] = MM::mfma(ones, pb[b][c], lacc[b]);
       __builtin_amdgcn_sched_barrier(0);  // slice 1's V reads wait for slice 0's products
     }
   };
@@ -1071,7 +1074,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
 #pragma unroll
       for (int b = 0; b < QPW; ++b) {
         xm[(2 * b) * 64] = m_run[b];
-        xm[(2 * b + 1) * 64] = l_part[b];
+        xm[(2 * b + 1) * 64] = lacc[b][0];
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1087,7 +1090,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       const float a0 = m_run[b] == -INFINITY ? 0.f : fast_exp2(m_run[b] - m_new);
       const float a1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - m_new);
       m_run[b] = m_new;
-      l_part[b] = l_part[b] * a0 + l1 * a1;
+      lacc[b][0] = lacc[b][0] * a0 + l1 * a1;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -1099,7 +1102,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   // ---- normalise and store (as paged_prefill_mfma)
 #pragma unroll
   for (int b = 0; b < QPW; ++b) {
-    const float l = cross_group_sum(l_part[b]);
+    const float l = lacc[b][0];
     if (qi[b] >= a.T) continue;
     if (a.part_keys > 0) {
       const int np = (a.start + qi[b] + a.part_keys) / a.part_keys;
