@@ -936,9 +936,13 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
 #pragma unroll
           for (int i = 0; i < 4; ++i) p[kb][i] = s[b][kb][i];
       } else {
+        // Defined here, so the compiler cannot hoist this path's index
+        // arithmetic above the branch into every full tile.
+        int g8 = 8 * g;
+        asm volatile("" : "+v"(g8));
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          const int k0 = 32 * (kb >> 1) + 8 * g + 4 * (kb & 1);  // within the tile
+          const int k0 = 32 * (kb >> 1) + g8 + 4 * (kb & 1);  // within the tile
           const uint32_t bits = (uint32_t)(vm >> k0) & 0xfu;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
