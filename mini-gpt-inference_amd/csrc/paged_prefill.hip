@@ -64,6 +64,20 @@ __device__ __forceinline__ float cross_group_sum(float x) {
   return x + shfl_xor32(x);
 }
 
+// The kernels take tile maxima over raw scores s (masked ones -inf) and
+// scale them afterwards, which needs a positive scale c. softmax(c s) =
+// softmax(|c| (-s)) for c < 0, and softmax(1 (0 s)) for c = 0. So the query
+// fragments are negated for c < 0 (exactly, by flipping the sign bit of every
+// T element of the 32-bit words) or zeroed for c = 0, and query_scale(c)
+// replaces c.
+template <typename T>
+__device__ __forceinline__ uint4 query_sign(uint4 x, float c) {
+  if (c == 0.f) return make_uint4(0, 0, 0, 0);
+  const uint32_t m = c < 0.f ? (sizeof(T) == 2 ? 0x80008000u : 0x80000000u) : 0u;
+  return make_uint4(x.x ^ m, x.y ^ m, x.z ^ m, x.w ^ m);
+}
+__device__ __forceinline__ float query_scale(float c) { return c == 0.f ? 1.f : fabsf(c); }
+
 // Element offsets of key `key`'s K and V rows (relative to the head's base
 // in the layer), or -1 for keys past the chunk or invalid table entries.
 struct KeyRows {
@@ -214,6 +228,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     for (int f = 0; f < NQF; ++f) {
       const int d = k16 ? 32 * f + 8 * g : 16 * f + 4 * g;
       qf[b][f] = (ok && d < a.D) ? *reinterpret_cast<const uint4*>(qrow + d) : make_uint4(0, 0, 0, 0);
+      qf[b][f] = query_sign<T>(qf[b][f], a.scale_log2);
     }
   }
 
@@ -325,15 +340,16 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
     }
 
     // ---- causal mask (diagonal tiles) and invalid-key mask, online softmax
-    // per query column. Raw scores s; the log2-domain score is s * scale_log2
-    // (scale > 0, so the maximum of raw scores gives the maximum of scaled ones).
+    // per query column. Raw scores s; the log2-domain score is
+    // s * query_scale(scale_log2) (the query carries the scale's sign, so the
+    // maximum of raw scores gives the maximum of scaled ones).
     // The tile's validity mask is wave-uniform: read it into scalar registers
     // so interior tiles take a branch with no masking work at all.
     const uint64_t vm_lds = slot_valid[vb];
     const uint32_t vm_lo = __builtin_amdgcn_readfirstlane((uint32_t)vm_lds);
     const uint32_t vm_hi = __builtin_amdgcn_readfirstlane((uint32_t)(vm_lds >> 32));
     const bool full = kt0 + kTileKeys - 1 <= wave_first && (vm_lo & vm_hi) == 0xffffffffu;
-    const float c = a.scale_log2;
+    const float c = query_scale(a.scale_log2);
     float p[QPW][4][4];
     if (full) {
 #pragma unroll
@@ -752,6 +768,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
     for (int f = 0; f < NQF; ++f) {
       const int d = 32 * f + 8 * g;
       qf[b][f] = (ok && d < a.D) ? *reinterpret_cast<const uint4*>(qrow + d) : make_uint4(0, 0, 0, 0);
+      qf[b][f] = query_sign<T>(qf[b][f], a.scale_log2);
     }
   }
 
@@ -897,7 +914,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
     va[db] = vbuf0 * TILEB + vr * ROWB + ((tr_q & 1) << 3) + (((2 * db + (tr_q >> 1)) ^ v_swz<CPR>(vr)) << 4);
-  const float cs = a.scale_log2;
+  const float cs = query_scale(a.scale_log2);  // the query carries the sign (query_sign)
 
   // QK^T and softmax of the tile in stage ST: packs P for the PV product.
   auto qk_softmax = [&](int kt0, uint64_t vm, int ST, uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {

@@ -370,3 +370,38 @@ def test_long_context_split_decode():
             other = hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer,
                                                   split_tokens=split)
             torch.testing.assert_close(other.float(), base.float(), **BF16_TOL)
+
+
+# ------------------------------------------------------------ any finite scale
+
+@pytest.mark.parametrize("scale", [-0.3, 0.0], ids=["neg", "zero"])
+@pytest.mark.parametrize("split", [0, 64], ids=["balanced", "partitions"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_any_finite_scale_matches_c_oracle(dtype, split, scale):
+    """mgi_paged_decode with a negative or zero scale (the torch wrapper
+    always passes 1/sqrt(D)) against the C oracle: the kernels scale scores
+    before taking maxima, so any finite scale is exact."""
+    B, H, D, S = 24, 8, 128, 16
+    g = torch.Generator().manual_seed(41)
+    ctx = torch.randint(0, 600, (B,), generator=g).tolist()
+    q, pool, tables, lens, layer = _small_case(B, H, D, S, ctx, dtype, seed=41)
+    dpool = fx.pool_to_device(pool, DEV)
+    qd, td, ld = q.to(DEV), tables.to(DEV), lens.to(DEV)
+    lib = hpd._native.lib()
+    L, N = dpool.k.shape[:2]
+    M = td.shape[1]
+    ws_bytes = int(lib.mgi_paged_decode_workspace_bytes(B, H, D, S, M, split))
+    ws = torch.full((max(ws_bytes, 4) // 4,), float("nan"), device=DEV)
+    out = torch.full_like(qd, float("nan"))
+    print(f"  hip decode scale={scale} split={split} B={B} H={H} D={D} dtype={dtype}", flush=True)
+    hpd._native.check(lib.mgi_paged_decode(
+        out.data_ptr(), hpd._native.strides(out), qd.data_ptr(), hpd._native.strides(qd),
+        dpool.k.data_ptr(), dpool.v.data_ptr(), hpd._native.strides(dpool.k), hpd._native.strides(dpool.v),
+        hpd._native.DTYPE_CODES[dtype], td.data_ptr(), hpd._native.strides(td), hpd._native.ITYPE_CODES[td.dtype],
+        ld.data_ptr(), ld.stride(0), hpd._native.ITYPE_CODES[ld.dtype],
+        B, H, D, S, N, M, L, layer, float(scale), split, ws.data_ptr(), ws_bytes, hpd._native.stream_handle(DEV)))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    want = c_oracle.paged_decode(*oracle_args(q, pool, tables, lens, layer), scale=scale)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, **tol_for(dtype))

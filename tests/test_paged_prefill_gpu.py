@@ -364,3 +364,57 @@ def test_bf16_runtime_hip_prefill_matches_sdpa_v2():
     diverged = _e2e.first_divergences(out["sdpa_v2"][0], out["hip"][0], margins)
     print(f"  hip prefill vs sdpa_v2, bf16: diverged {diverged}", flush=True)
     assert all(m < 0.1 for _, _, m in diverged), diverged
+
+
+# ------------------------------------------------------------ any finite scale
+
+def run_hip_scaled(q, pool, table, start, layer, scale):
+    """mgi_paged_prefill through the C ABI with an explicit scale (the torch
+    binding always passes 1/sqrt(D))."""
+    lib = hpd._native.lib()
+    T, H, D = q.shape
+    L, N, S = pool.k.shape[:3]
+    code = hpd._native.DTYPE_CODES[q.dtype]
+    tbl = table.to(DEV)
+    ws_bytes = int(lib.mgi_paged_prefill_workspace_bytes(start, T, H, D, code))
+    ws = torch.full((max(ws_bytes, 4) // 4,), float("nan"), device=DEV)
+    out = torch.full_like(q, float("nan"))
+    print(f"  hip prefill scale={scale} start={start} T={T} H={H} D={D} dtype={q.dtype}", flush=True)
+    hpd._native.check(lib.mgi_paged_prefill(
+        out.data_ptr(), hpd._native.strides(out), q.data_ptr(), hpd._native.strides(q),
+        pool.k.data_ptr(), pool.v.data_ptr(), hpd._native.strides(pool.k), hpd._native.strides(pool.v),
+        code, tbl.data_ptr(), tbl.stride(0), hpd._native.ITYPE_CODES[tbl.dtype], tbl.shape[0],
+        start, T, H, D, S, N, L, layer, float(scale), ws.data_ptr(), ws_bytes,
+        hpd._native.stream_handle(DEV)))
+    torch.cuda.synchronize()
+    return out
+
+
+SCALE_CASES = [
+    # dtype, start, T, H, D, kernel configuration, keys per partition (0: whole)
+    (torch.bfloat16, 100, 130, 4, 128, "1422", "0"),
+    (torch.bfloat16, 100, 130, 4, 128, "412", "0"),
+    (torch.bfloat16, 100, 130, 4, 128, "0", "0"),
+    (torch.float16, 100, 130, 4, 128, "-1", "0"),
+    (torch.float32, 37, 50, 4, 64, "-1", "0"),
+    (torch.bfloat16, 1000, 200, 4, 128, "-1", "128"),
+]
+
+
+@pytest.mark.parametrize("scale", [-1 / math.sqrt(128), -0.3, 0.0, 0.3], ids=["neg_rsqrt", "neg", "zero", "pos"])
+@pytest.mark.parametrize("dtype,start,T,H,D,config,split", SCALE_CASES,
+                         ids=["bf16_1422", "bf16_412", "bf16_mfma", "f16", "f32", "bf16_split"])
+def test_any_finite_scale_matches_oracle(monkeypatch, dtype, start, T, H, D, config, split, scale):
+    """softmax(scale * q.k) for negative, zero and positive scales: the kernels
+    take maxima over raw scores, so a negative scale is carried by the query's
+    sign; the oracle scales before its maximum."""
+    if config != "-1":
+        monkeypatch.setenv("MINIVLLM_HIP_PREFILL_TR", config)
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_SPLIT_KEYS", split)
+    qkv, pool, table, layer = prefill_case(start, T, H, D, 16, dtype, seed=31)
+    q = qkv.to(DEV)[:, 0]
+    got = run_hip_scaled(q, pool, table, start, layer, scale).float().cpu().numpy()
+    want = ora.paged_prefill(fx.to_numpy(q), fx.to_numpy(pool.k), fx.to_numpy(pool.v), table.numpy(),
+                             start, layer, scale=scale)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, **TOL[dtype])
