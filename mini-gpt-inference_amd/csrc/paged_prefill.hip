@@ -888,14 +888,21 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   // 16-row block of ones in place of V^T, so each lane holds the sum over
   // every key of its query column, four times (no VALU adds, no cross-lane
   // sum at the end). The sum is of the 2-byte P the output accumulates.
+  // Softmax state per 16-row block: the reference maximum m_run (log2
+  // domain), neg_m = -m_run (0 while m_run = -inf), and thr = (m_run +
+  // slack) / scale, the raw-score maximum past which a tile rescales (-inf
+  // while m_run = -inf). neg_m and thr change only on a rescale, so a tile
+  // that does not rescale spends one compare per block on the check.
   f32x4_t oacc[QPW][NDB], lacc[QPW];
-  float m_run[QPW];
+  float m_run[QPW], neg_m[QPW], thr[QPW];
 #pragma unroll
   for (int b = 0; b < QPW; ++b) {
 #pragma unroll
     for (int i = 0; i < NDB; ++i) oacc[b][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     lacc[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m_run[b] = -INFINITY;
+    neg_m[b] = 0.f;
+    thr[b] = -INFINITY;
   }
   const uint32_t one2 = MM::pack2(1.f, 1.f);
   const uint4 ones = make_uint4(one2, one2, one2, one2);
@@ -915,6 +922,7 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   for (int db = 0; db < NDB; ++db)
     va[db] = vbuf0 * TILEB + vr * ROWB + ((tr_q & 1) << 3) + (((2 * db + (tr_q >> 1)) ^ v_swz<CPR>(vr)) << 4);
   const float cs = query_scale(a.scale_log2);  // the query carries the sign (query_sign)
+  const float inv_cs = 1.f / cs;
 
   // QK^T and softmax of the tile in stage ST: packs P for the PV product.
   auto qk_softmax = [&](int kt0, uint64_t vm, int ST, uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
@@ -973,21 +981,20 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mt = fmaxf(mt, p[kb][i]);
-      mt *= cs;
-      if (__builtin_amdgcn_ballot_w64(mt > m_run[b] + kRescaleSlack) != 0) {
-        mt = cross_group_max(mt);
-        const float m_new = fmaxf(m_run[b], mt);
+      if (__builtin_amdgcn_ballot_w64(mt > thr[b]) != 0) {
+        const float m_new = fmaxf(m_run[b], cross_group_max(mt) * cs);
         const float alpha = m_run[b] == -INFINITY ? 0.f : fast_exp2(m_run[b] - m_new);
         m_run[b] = m_new;
+        neg_m[b] = m_new == -INFINITY ? 0.f : -m_new;
+        thr[b] = m_new == -INFINITY ? -INFINITY : (m_new + kRescaleSlack) * inv_cs;
         lacc[b] *= alpha;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) oacc[b][db] *= alpha;
       }
-      const float neg_m = m_run[b] == -INFINITY ? 0.f : -m_run[b];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[kb][i] = fast_exp2(fmaf(p[kb][i], cs, neg_m));
+        for (int i = 0; i < 4; ++i) p[kb][i] = fast_exp2(fmaf(p[kb][i], cs, neg_m[b]));
 #pragma unroll
       for (int c = 0; c < 2; ++c)
         pb[b][c] = make_uint4(MM::pack2(p[2 * c][0], p[2 * c][1]), MM::pack2(p[2 * c][2], p[2 * c][3]),

@@ -401,7 +401,8 @@ SCALE_CASES = [
 ]
 
 
-@pytest.mark.parametrize("scale", [-1 / math.sqrt(128), -0.3, 0.0, 0.3], ids=["neg_rsqrt", "neg", "zero", "pos"])
+@pytest.mark.parametrize("scale", [-1 / math.sqrt(128), -0.3, 0.0, 0.3, 4.0],
+                         ids=["neg_rsqrt", "neg", "zero", "pos", "large"])
 @pytest.mark.parametrize("dtype,start,T,H,D,config,split", SCALE_CASES,
                          ids=["bf16_1422", "bf16_412", "bf16_mfma", "f16", "f32", "bf16_split"])
 def test_any_finite_scale_matches_oracle(monkeypatch, dtype, start, T, H, D, config, split, scale):
