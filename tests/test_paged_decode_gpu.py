@@ -405,3 +405,47 @@ def test_any_finite_scale_matches_c_oracle(dtype, split, scale):
     want = c_oracle.paged_decode(*oracle_args(q, pool, tables, lens, layer), scale=scale)
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got, want, **tol_for(dtype))
+
+
+@pytest.mark.parametrize("split", [0, 64], ids=["balanced", "partitions"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_strided_outputs_match_contiguous(dtype, split):
+    """mgi_paged_decode writes through any output strides: a head-major view,
+    an odd row stride and an element stride of 2 give the contiguous output
+    bit for bit, and the columns between the elements stay untouched."""
+    B, H, D, S = 16, 8, 128, 16
+    g = torch.Generator().manual_seed(43)
+    ctx = torch.randint(1, 900, (B,), generator=g).tolist()
+    q, pool, tables, lens, layer = _small_case(B, H, D, S, ctx, dtype, seed=43)
+    dpool = fx.pool_to_device(pool, DEV)
+    qd, td, ld = q.to(DEV), tables.to(DEV), lens.to(DEV)
+    lib = hpd._native.lib()
+    L, N = dpool.k.shape[:2]
+    M = td.shape[1]
+    ws_bytes = int(lib.mgi_paged_decode_workspace_bytes(B, H, D, S, M, split))
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=DEV)
+
+    def call(out):
+        print(f"  hip decode split={split} dtype={dtype} out strides={tuple(out.stride())}", flush=True)
+        hpd._native.check(lib.mgi_paged_decode(
+            out.data_ptr(), hpd._native.strides(out), qd.data_ptr(), hpd._native.strides(qd),
+            dpool.k.data_ptr(), dpool.v.data_ptr(), hpd._native.strides(dpool.k),
+            hpd._native.strides(dpool.v), hpd._native.DTYPE_CODES[dtype], td.data_ptr(),
+            hpd._native.strides(td), hpd._native.ITYPE_CODES[td.dtype], ld.data_ptr(), ld.stride(0),
+            hpd._native.ITYPE_CODES[ld.dtype], B, H, D, S, N, M, L, layer, 1.0 / math.sqrt(D), split,
+            ws.data_ptr(), ws_bytes, hpd._native.stream_handle(DEV)))
+        torch.cuda.synchronize()
+        return out
+
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    base = call(torch.full_like(qd, float("nan")))
+    head_major = call(torch.full((H, B, D), float("nan"), device=DEV, dtype=dtype).permute(1, 0, 2))
+    wide = torch.full((B, H, D + 5), float("nan"), device=DEV, dtype=dtype)
+    odd = call(wide[..., :D])
+    strided = torch.full((B, H, 2 * D), float("nan"), device=DEV, dtype=dtype)
+    every_other = call(strided[..., ::2])
+    for got in (head_major, odd, every_other):
+        assert torch.equal(got.contiguous().view(bits), base.view(bits))
+    assert torch.isnan(wide[..., D:]).all() and torch.isnan(strided[..., 1::2]).all()
+    want = c_oracle.paged_decode(*oracle_args(q, pool, tables, lens, layer))
+    np.testing.assert_allclose(base.float().cpu().numpy(), want, **tol_for(dtype))

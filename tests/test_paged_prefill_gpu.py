@@ -368,9 +368,9 @@ def test_bf16_runtime_hip_prefill_matches_sdpa_v2():
 
 # ------------------------------------------------------------ any finite scale
 
-def run_hip_scaled(q, pool, table, start, layer, scale):
+def run_hip_scaled(q, pool, table, start, layer, scale, out=None):
     """mgi_paged_prefill through the C ABI with an explicit scale (the torch
-    binding always passes 1/sqrt(D))."""
+    binding always passes 1/sqrt(D)), into `out` (any strides) if given."""
     lib = hpd._native.lib()
     T, H, D = q.shape
     L, N, S = pool.k.shape[:3]
@@ -378,8 +378,10 @@ def run_hip_scaled(q, pool, table, start, layer, scale):
     tbl = table.to(DEV)
     ws_bytes = int(lib.mgi_paged_prefill_workspace_bytes(start, T, H, D, code))
     ws = torch.full((max(ws_bytes, 4) // 4,), float("nan"), device=DEV)
-    out = torch.full_like(q, float("nan"))
-    print(f"  hip prefill scale={scale} start={start} T={T} H={H} D={D} dtype={q.dtype}", flush=True)
+    if out is None:
+        out = torch.full_like(q, float("nan"))
+    print(f"  hip prefill scale={scale} start={start} T={T} H={H} D={D} dtype={q.dtype} "
+          f"out strides={tuple(out.stride())}", flush=True)
     hpd._native.check(lib.mgi_paged_prefill(
         out.data_ptr(), hpd._native.strides(out), q.data_ptr(), hpd._native.strides(q),
         pool.k.data_ptr(), pool.v.data_ptr(), hpd._native.strides(pool.k), hpd._native.strides(pool.v),
@@ -419,3 +421,26 @@ def test_any_finite_scale_matches_oracle(monkeypatch, dtype, start, T, H, D, con
                              start, layer, scale=scale)
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got, want, **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_strided_outputs(dtype):
+    """The output through any strides: a head-major view keeps the matrix-core
+    kernels (16-byte strides) and matches the contiguous output bit for bit;
+    an odd row stride takes the generic path and matches the oracle."""
+    start, T, H, D = 60, 90, 4, 128
+    qkv, pool, table, layer = prefill_case(start, T, H, D, 16, dtype, seed=37)
+    q = qkv.to(DEV)[:, 0]
+    scale = 1 / math.sqrt(D)
+    base = run_hip_scaled(q, pool, table, start, layer, scale)
+    head_major = torch.full((H, T, D), float("nan"), device=DEV, dtype=dtype).permute(1, 0, 2)
+    got = run_hip_scaled(q, pool, table, start, layer, scale, out=head_major)
+    assert torch.equal(got.contiguous().view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       base.view(torch.int16 if dtype != torch.float32 else torch.int32))
+    wide = torch.full((T, H, D + 3), float("nan"), device=DEV, dtype=dtype)
+    odd = wide[..., :D]
+    got = run_hip_scaled(q, pool, table, start, layer, scale, out=odd).float().cpu().numpy()
+    want = ora.paged_prefill(fx.to_numpy(q), fx.to_numpy(pool.k), fx.to_numpy(pool.v), table.numpy(),
+                             start, layer)
+    np.testing.assert_allclose(got, want, **TOL[dtype])
+    assert torch.isnan(wide[..., D:]).all(), "the padding columns must stay untouched"
