@@ -571,9 +571,14 @@ __global__ __launch_bounds__(64 * WAVES) void paged_prefill_mfma(const PrefillAr
 
 // ------------------------------------------------------------------------
 // Direct-to-LDS variant (2-byte types, head dims 64 and 128, power-of-two
-// block sizes of at least 16). Same grid mapping, numerics and outputs as
+// block sizes of at least 16). Same grid mapping, softmax and outputs as
 // paged_prefill_mfma; what changes is how key tiles reach the matrix cores
-// and how little per-tile work the wavefronts spend on it:
+// and how little per-tile VALU work the wavefronts spend (VALU issue, not
+// the matrix cores, bounds this kernel):
+//   * The softmax denominators come out of the PV products (a block of ones
+//     beside V^T), as sums of the 2-byte P the outputs accumulate, and a
+//     tile's rescale check is one compare of its raw maximum per 16-row
+//     block against a threshold kept with the state.
 //   * A key tile is 64 keys = four 16-key granules, and a granule lies in one
 //     pool block (S is a power of two >= 16). The workgroup keeps a window of
 //     the block table in LDS as one int per granule: G = block * (S / 16) +
