@@ -112,6 +112,27 @@ def time_steps(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def warm_up(fn, ms: float = 50.0, cap: int = 2000) -> None:
+    """Untimed back-to-back calls of fn for about `ms` of GPU time (at most
+    `cap` calls): under sustained matrix-core load the GPU's clocks take tens
+    of milliseconds to settle, and a few warm-up calls leave the first timed
+    ones 10-20 % slow."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    fn()
+    end.record()
+    torch.cuda.synchronize()
+    one = max(start.elapsed_time(end), 1e-3)
+    for _ in range(min(cap, int(ms / one))):
+        fn()
+    torch.cuda.synchronize()
+
+
 def time_calls(fn, steps: int, warmup: int) -> dict:
     """Per-call HIP event pairs on the current stream (the stream the kernels
     launch on), `steps` calls after `warmup` untimed ones, bracketed by device
@@ -398,6 +419,7 @@ def prefill_line(dev, start: int, T: int, H: int = 16, D: int = 128, steps: int 
     """Paged prefill attention of one bf16 chunk (T queries after a cached
     prefix of `start` tokens, block size 16, scattered table): the HIP kernel
     against the fp32 gather + SDPA of prefill mode sdpa_v2 on the same GPU.
+    The HIP calls are timed after about 50 ms of untimed ones (warm_up).
     FLOPs are the causal algorithmic count 4*H*D*sum_i (start + i + 1)."""
     import types
 
@@ -418,6 +440,7 @@ def prefill_line(dev, start: int, T: int, H: int = 16, D: int = 128, steps: int 
     qkv = torch.randn(1, T, 3, H, D, device=dev).to(torch.bfloat16)
     q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
     tdev = table.to(dev)
+    warm_up(lambda: hpd.paged_prefill_hip(q[0], pool, tdev, start, 0))
     hip_ms = time_steps(lambda: hpd.paged_prefill_hip(q[0], pool, tdev, start, 0), steps, 3)
     attn = KVCacheCausalSelfAttention(H * D, H, start + T).to(dev)
     seq = types.SimpleNamespace(block_table=table.tolist())
@@ -906,6 +929,13 @@ def main() -> None:
             for start, T in ((0, 512), (2048, 2048), (4096, 256)):
                 key = f"prefill_bf16_start{start}_T{T}_H16_D128"
                 extras[key] = prefill_line(dev, start, T)
+                log(f"extra {key}: {extras[key]}")
+            if not args.no_extras:
+                # The same 2048 rows after a long prefix: every query tile's
+                # chain is nearly as long, so this shows the kernel's steady
+                # state without the causal imbalance of the chunk above.
+                key = "prefill_bf16_start16384_T2048_H16_D128"
+                extras[key] = prefill_line(dev, 16384, 2048)
                 log(f"extra {key}: {extras[key]}")
             torch.cuda.empty_cache()
 
