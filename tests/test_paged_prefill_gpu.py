@@ -167,13 +167,14 @@ def _tr_case(start, T, H, D, S, dtype):
 
 @pytest.mark.parametrize("config", TR_CONFIGS)
 @pytest.mark.parametrize("start,T,H,D,S", TR_CASES)
-def test_prefill_kernel_configs_match_oracle(monkeypatch, start, T, H, D, S, config):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_prefill_kernel_configs_match_oracle(monkeypatch, dtype, start, T, H, D, S, config):
     monkeypatch.setenv("MINIVLLM_HIP_PREFILL_TR", config)
-    q, pool, table, layer, want = _tr_case(start, T, H, D, S, torch.bfloat16)
+    q, pool, table, layer, want = _tr_case(start, T, H, D, S, dtype)
     print(f"  config {config}", flush=True)
     got = run_hip(q, pool, table, start, layer).float().cpu().numpy()
     assert np.isfinite(got).all()
-    np.testing.assert_allclose(got, want, **BF16_TOL)
+    np.testing.assert_allclose(got, want, **TOL[dtype])
 
 
 @pytest.mark.parametrize("config", TR_CONFIGS[1:])
