@@ -170,25 +170,37 @@ def run_to_completion(rt: MiniRuntime, seqs, max_steps: int = 100000, on_step=No
 GOLDEN_C1 = json.loads((Path(__file__).resolve().parent / "golden" / "c1_greedy_tokens.json").read_text())
 
 
-def run_c1(case: dict, device, backend: str, prefill_mode: str | None = None):
-    """Runs one golden case; returns (generated tokens per request, runtime).
-
-    prefill_mode overrides the recorded configuration's prefill mode (the
-    golden tokens were produced with it)."""
+def make_c1_model(device, prefill_mode: str | None = None) -> MiniGPT:
+    """The golden configuration's Mini-GPT (seed 0, fp32); prefill_mode
+    overrides the recorded configuration's prefill mode."""
     cfg = GOLDEN_C1["config"]
     torch.manual_seed(cfg["seed"])
     model = MiniGPT(n_embd=cfg["n_embd"], n_head=cfg["n_head"], vocab_size=cfg["vocab_size"],
                     block_size=cfg["block_size"], dropout=0.0, n_layer=cfg["n_layer"]).eval().to(device)
     model.set_prefill_fastpath_mode(prefill_mode or cfg["prefill_mode"])
-    model.set_decode_attention_backend(backend)
+    return model
+
+
+def c1_pool_blocks(case: dict, kv_factor: float = 1.0) -> int:
+    """Pool size of a golden case: every request's whole run
+    (B * ceil((P + out - 1) / S) blocks) times kv_factor, at least one
+    request's, as experiments/gpu_e2e_runtime.py:96-103 sizes it."""
+    cfg = GOLDEN_C1["config"]
+    per = math.ceil((case["prompt_len"] + cfg["output_len"] - 1) / cfg["block_size_kv"])
+    return max(per, math.ceil(case["batch"] * per * kv_factor))
+
+
+def make_c1_runtime(model: MiniGPT, case: dict, device, policy: str = "conservative", kv_factor: float = 1.0):
+    """A runtime over one golden case's requests on a NaN-filled pool of
+    c1_pool_blocks(case, kv_factor) blocks; returns (runtime, sequences)."""
+    cfg = GOLDEN_C1["config"]
     B, P, S = case["batch"], case["prompt_len"], cfg["block_size_kv"]
-    blocks = B * math.ceil((P + cfg["output_len"] - 1) / S)
-    assert blocks == case["num_blocks"]
+    blocks = c1_pool_blocks(case, kv_factor)
     manager = BlockManager(num_blocks=blocks, block_size=S)
     rt = MiniRuntime.__new__(MiniRuntime)
     rt.block_manager = manager
     rt.scheduler = Scheduler(manager, max_running=B, max_num_batched_tokens=cfg["token_budget"],
-                             preemption_policy="conservative")
+                             preemption_policy=policy)
     pool = KVBlockPool(n_layer=cfg["n_layer"], num_blocks=blocks, block_size=S, n_head=cfg["n_head"],
                        head_dim=cfg["n_embd"] // cfg["n_head"], device=device)
     pool.k.fill_(float("nan"))
@@ -199,13 +211,35 @@ def run_c1(case: dict, device, backend: str, prefill_mode: str | None = None):
                           max_tokens=P + cfg["output_len"]) for i in range(B)]
     for s in seqs:
         rt.add_request(s)
+    return rt, seqs
+
+
+def step_c1(rt: MiniRuntime, seqs, check: bool = True) -> None:
+    """Steps a golden-case runtime to completion (block-manager invariants
+    after every step unless ``check`` is off)."""
     with torch.inference_mode():
         for _ in range(1000):
             if all(s.status == Status.FINISHED for s in seqs):
                 break
             rt.step()
-            manager.check_invariants([s for s in seqs if s.status != Status.FINISHED])
+            if check:
+                rt.block_manager.check_invariants([s for s in seqs if s.status != Status.FINISHED])
     assert all(s.status == Status.FINISHED for s in seqs)
+
+
+def run_c1(case: dict, device, backend: str, prefill_mode: str | None = None, policy: str = "conservative",
+           kv_factor: float = 1.0):
+    """Runs one golden case; returns (generated tokens per request, runtime).
+
+    prefill_mode overrides the recorded configuration's prefill mode (the
+    golden tokens were produced with it); policy and kv_factor size the pool
+    and choose the preemption policy (the golden run: "conservative", 1.0)."""
+    model = make_c1_model(device, prefill_mode)
+    model.set_decode_attention_backend(backend)
+    if kv_factor == 1.0:
+        assert c1_pool_blocks(case) == case["num_blocks"]
+    rt, seqs = make_c1_runtime(model, case, device, policy, kv_factor)
+    step_c1(rt, seqs)
     return [s.generated_tokens for s in seqs], rt
 
 
@@ -256,13 +290,57 @@ def _token_slots(seq: SequenceState, S: int) -> list[int]:
     return [t[p // S] * S + p % S for p in range(seq.length)]
 
 
-# Lock-step criterion of the full configuration in bf16 (see Lockstep and
-# test_e2e_lockstep_gpu.py), scaled by each row's largest magnitude: logits
-# and decode-written KV within 2^-6 + 2^-6 * max|row| (four bf16 ulps of the
-# row's largest entry, plus 2^-6); a token may diverge only where the
-# reference's top-2 margin is below twice its row's logit bound.
+# Lock-step criteria of the full configuration in bf16 (see Lockstep and
+# test_e2e_lockstep_gpu.py), scaled by each row's largest magnitude:
+# |hip - ref| <= atol + rtol * max|ref row| on logits and on decode-written KV;
+# a token may differ only where the reference's top-2 margin is below twice
+# its row's logit bound, and the reference's token is then forced into the
+# HIP runtime.
+#   * against the reference backend as it runs in bf16 (online_v1 keeps its
+#     running max, sum and output in bf16, rounded at every block): 2^-6 +
+#     2^-6 * max|row|, four bf16 ulps of the row's largest entry plus 2^-6;
+#   * against online_v1 run on float32 copies of q, K and V, its output
+#     rounded to bf16 (the HIP kernel's own arithmetic: fp32 accumulation of
+#     bf16 data): the two differ by the order of fp32 sums and by the
+#     exponential's last bits, which flip the bf16 rounding of an attention
+#     output now and then; every later bf16 rounding (GEMM outputs, residual
+#     stream, logits) then moves by whole ulps, so a logit differs by at
+#     least one ulp of its own size once anything upstream differs. The
+#     bound is three quarters of the bf16 one: 0.75 * 2^-6 (1 + max|row|).
 C5_BF16_LOCKSTEP = dict(logit_tol=(2.0 ** -6, 2.0 ** -6), tie_margin=None, kv_tol=(2.0 ** -6, 2.0 ** -6),
                         row_scaled=True)
+_FP32_REF_TOL = 0.75 * 2.0 ** -6
+C5_FP32_REF_LOCKSTEP = dict(logit_tol=(_FP32_REF_TOL, _FP32_REF_TOL), tie_margin=None,
+                            kv_tol=(_FP32_REF_TOL, _FP32_REF_TOL), row_scaled=True)
+
+
+class _Upcast:
+    """Indexing returns a float32 copy of the indexed part of a pool tensor."""
+
+    def __init__(self, t: torch.Tensor):
+        self.t = t
+
+    def __getitem__(self, idx):
+        return self.t[idx].float()
+
+
+class _Float32Pool:
+    """The k / v / block_size view of a KVBlockPool that paged_attention_batch_online_v1
+    reads, with every gathered block converted to float32."""
+
+    def __init__(self, pool: KVBlockPool):
+        self.k, self.v, self.block_size = _Upcast(pool.k), _Upcast(pool.v), pool.block_size
+
+
+def online_v1_fp32(q, pool, block_tables, context_lengths, layer_idx):
+    """The package's online_v1 on float32 copies of q and of each gathered
+    K/V block (fp32 accumulation of the stored bf16 values); the output is
+    rounded back to q's dtype."""
+    from minivllm.paged_attention_batch import paged_attention_batch_online_v1
+
+    out = paged_attention_batch_online_v1(q=q.float(), pool=_Float32Pool(pool), block_tables=block_tables,
+                                          context_lengths=context_lengths, layer_idx=layer_idx)
+    return out.to(q.dtype)
 
 
 class Lockstep:
@@ -271,27 +349,29 @@ class Lockstep:
     experiments/gpu_day6_runtime_decode_ab.py:59-130 steps its two backends.
     Prefill uses the model's prefill mode in both, so the only difference
     between the runs is the decode attention backend ("reference" = the
-    PyTorch online-softmax path, "hip" = kv_append + the HIP decode kernel).
+    PyTorch online-softmax path, or ``ref_attention`` in its place when
+    given; "hip" = kv_append + the HIP decode kernel).
 
     ``step()`` advances both runtimes by one iteration and checks:
       * identical schedules (prefill chunks, decode batch order), sequence
         states (status, length, prompt position, block table) and lifecycle
-        counts -- the schedule is token-independent, so this holds even
-        after a token stream diverges;
-      * decode logits of every row whose inputs still agree within
-        ``logit_tol`` = (atol, rtol): |hip - ref| <= atol + rtol * |ref|
-        elementwise, or, with ``row_scaled``, atol + rtol * max|ref row|
-        (rounding of the hidden state moves every logit of a row in
-        proportion to the row's scale, not to the logit's own size);
-      * greedy tokens identical, except that a stream may diverge where the
-        reference's top-2 logit margin is below ``tie_margin`` (None: twice
-        that row's logit bound, the largest gap two logits each moved by the
-        bound can close); the diverged sequence is left out of the logit and
-        KV checks from then on (its inputs differ);
-      * logical KV of every active, not diverged sequence read through its
-        block table: bit-identical in layer 0 (its input is the token and
-        position embedding alone) and at every position the current prefill
-        wrote (prefill is shared and deterministic), within ``kv_tol`` at
+        counts;
+      * decode logits of every row within ``logit_tol`` = (atol, rtol):
+        |hip - ref| <= atol + rtol * |ref| elementwise, or, with
+        ``row_scaled``, atol + rtol * max|ref row| (rounding of the hidden
+        state moves every logit of a row in proportion to the row's scale,
+        not to the logit's own size);
+      * greedy tokens identical, except where the reference's top-2 logit
+        margin is below ``tie_margin`` (None: twice that row's logit bound,
+        the largest gap two logits each moved by the bound can close). There
+        the reference's token is written into the HIP runtime's sequence
+        (its last generated token and its next decode input) and the event is
+        recorded in ``forced``, so both runtimes keep decoding the same
+        tokens and every later row stays in the logit and KV checks;
+      * logical KV of every active sequence read through its block table:
+        bit-identical in layer 0 (its input is the token and position
+        embedding alone) and at every position the current prefill wrote
+        (prefill is shared and deterministic), within ``kv_tol`` at
         positions decode wrote in later layers (the decode attention outputs
         differ in rounding; ``row_scaled`` scales by each token's [H, D] row
         in that layer). ``kv_tol=None`` checks through
@@ -303,27 +383,46 @@ class Lockstep:
 
     def __init__(self, spec: RuntimeSpec, model: MiniGPT, prompts, device, dtype, *,
                  logit_tol: tuple[float, float], tie_margin: float | None, kv_tol: tuple[float, float] | None,
-                 row_scaled: bool = False):
+                 row_scaled: bool = False, ref_attention=None):
         self.model = model
         self.logit_tol, self.tie_margin, self.kv_tol = logit_tol, tie_margin, kv_tol
         self.row_scaled = row_scaled
+        self.ref_attention = ref_attention
         self.ref = _Probe(*make_runtime(spec, model, prompts, device, dtype))
         self.hip = _Probe(*make_runtime(spec, model, prompts, device, dtype))
-        self.diverged: dict[str, tuple[int, int, float]] = {}   # seq_id -> (step, token index, margin)
+        self.forced: list[tuple[int, str, int, float]] = []   # (step, seq_id, token index, ref margin)
         # max_*_ratio: the largest deviation as a fraction of its bound (<= 1 passes).
-        self.stats = {"steps": 0, "decode_rows_checked": 0, "max_logit_abs": 0.0, "max_logit_ratio": 0.0,
-                      "kv_tokens_checked": 0, "kv_exact_tokens": 0, "max_kv_abs": 0.0, "max_kv_ratio": 0.0,
-                      "preemptions": 0, "recomputed_seqs": set()}
+        self.stats = {"steps": 0, "decode_rows": 0, "decode_rows_checked": 0, "max_logit_abs": 0.0,
+                      "max_logit_ratio": 0.0, "kv_tokens_checked": 0, "kv_exact_tokens": 0, "max_kv_abs": 0.0,
+                      "max_kv_ratio": 0.0, "preemptions": 0, "recomputed_seqs": set()}
 
     @property
     def finished(self) -> bool:
         return all(s.status == Status.FINISHED for s in self.ref.seqs)
 
+    @property
+    def forced_streams(self) -> set[str]:
+        return {sid for _, sid, _, _ in self.forced}
+
+    def _step_reference(self) -> None:
+        if self.ref_attention is None:
+            self.ref.step()
+            return
+        import minivllm.attention as attention_mod
+
+        inner = attention_mod.paged_attention_batch_online_v1
+        attention_mod.paged_attention_batch_online_v1 = self.ref_attention
+        try:
+            self.ref.step()
+        finally:
+            attention_mod.paged_attention_batch_online_v1 = inner
+
     def step(self) -> None:
         step = self.stats["steps"] + 1
-        for backend, probe in (("reference", self.ref), ("hip", self.hip)):
-            self.model.set_decode_attention_backend(backend)
-            probe.step()
+        self.model.set_decode_attention_backend("reference")
+        self._step_reference()
+        self.model.set_decode_attention_backend("hip")
+        self.hip.step()
         self.stats["steps"] = step
         a, b = self.ref, self.hip
         if a.plan != b.plan:
@@ -336,6 +435,7 @@ class Lockstep:
             if sa[key] != sb[key]:
                 raise AssertionError(f"step {step}: {key} {sa[key]} vs {sb[key]}")
         self.stats["preemptions"] = sa["preemptions"]
+        self.stats["decode_rows"] = sa["decode_tokens"]
         for sid, _, _ in a.plan[0]:
             if a.by_id[sid].num_preemptions:
                 self.stats["recomputed_seqs"].add(sid)
@@ -358,24 +458,19 @@ class Lockstep:
             raise AssertionError(f"step {step}: decode ran in one runtime only")
         atol, rtol = self.logit_tol
         if a.logits is not None:
-            keep = [i for i, sid in enumerate(a.decoded) if sid not in self.diverged]
-            if keep:
-                rows = torch.tensor(keep, device=a.logits.device)
-                ra, rb = a.logits.index_select(0, rows), b.logits.index_select(0, rows)
-                diff = (ra - rb).abs()
-                scale = ra.abs().amax(dim=1, keepdim=True) if self.row_scaled else ra.abs()
-                ratio = (diff / (atol + rtol * scale)).max().item()
-                self.stats["max_logit_abs"] = max(self.stats["max_logit_abs"], diff.max().item())
-                self.stats["max_logit_ratio"] = max(self.stats["max_logit_ratio"], ratio)
-                self.stats["decode_rows_checked"] += len(keep)
-                if ratio > 1:
-                    raise AssertionError(f"step {step}: decode logits differ by {diff.max().item():.4g} "
-                                         f"(tolerance atol {atol} + rtol {rtol} * |ref|)")
-        # Tokens: every stream not yet diverged must agree; a new divergence
-        # is allowed only at a near tie of the reference's logits.
+            diff = (a.logits - b.logits).abs()
+            scale = a.logits.abs().amax(dim=1, keepdim=True) if self.row_scaled else a.logits.abs()
+            ratio = (diff / (atol + rtol * scale)).max().item()
+            self.stats["max_logit_abs"] = max(self.stats["max_logit_abs"], diff.max().item())
+            self.stats["max_logit_ratio"] = max(self.stats["max_logit_ratio"], ratio)
+            self.stats["decode_rows_checked"] += a.logits.shape[0]
+            if ratio > 1:
+                raise AssertionError(f"step {step}: decode logits differ by {diff.max().item():.4g} "
+                                     f"(tolerance atol {atol} + rtol {rtol} * |ref|)")
+        # Tokens: every stream agrees up to this step (earlier differences were
+        # forced away); a token drawn in this step may differ only at a near
+        # tie of the reference's logits, and is then replaced by the reference's.
         for x in a.seqs:
-            if x.seq_id in self.diverged:
-                continue
             y = b.by_id[x.seq_id]
             if x.generated_tokens == y.generated_tokens:
                 continue
@@ -391,11 +486,14 @@ class Lockstep:
             if margin >= allowed:
                 raise AssertionError(f"step {step}: {x.seq_id} token {k} differs at reference top-2 "
                                      f"margin {margin:.4g} (allowed only below {allowed:.4g})")
-            self.diverged[x.seq_id] = (step, k, margin)
+            if y.last_token != y.generated_tokens[-1] or x.last_token != x.generated_tokens[-1]:
+                raise AssertionError(f"step {step}: {x.seq_id} pending token is not its last generated one")
+            y.generated_tokens[-1] = x.generated_tokens[-1]
+            y.last_token = x.last_token
+            self.forced.append((step, x.seq_id, k, margin))
 
     def _check_kv(self, step: int) -> None:
-        live = [x for x in self.ref.seqs
-                if x.status != Status.FINISHED and x.length > 0 and x.seq_id not in self.diverged]
+        live = [x for x in self.ref.seqs if x.status != Status.FINISHED and x.length > 0]
         if not live:
             return
         if self.kv_tol is None:

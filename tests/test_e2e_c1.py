@@ -6,6 +6,14 @@ golden/c1_greedy_tokens.json by golden/make_c1_greedy_tokens.py.
 
 CPU: the PyTorch "reference" decode backend. GPU: the HIP backend
 (kv_append + paged decode kernels) on cuda:0.
+
+Forced recompute preemption: the batch-4 cases on a pool of half the blocks
+the whole run needs ("recompute" policy, capacity factor 0.5 as
+experiments/gpu_e2e_runtime.py:96-103 sizes it) preempt one request once and
+replay 16 KV tokens, the lifecycle of the reference's published
+forced-preemption row (README.md:221-223: 1 preemption, 16 replayed KV
+tokens, identical tokens and lifecycle counts in both backends). The token
+streams equal the golden ones of the run without preemption.
 """
 from __future__ import annotations
 
@@ -39,3 +47,38 @@ def test_hip_backend_matches_golden_tokens_gpu(case):
     tokens, rt = run_c1(case, "cuda", "hip")
     assert tokens == case["outputs"]
     assert rt.iteration == case["iterations"]
+
+
+FORCED = [c for c in GOLDEN["cases"] if c["batch"] == 4]
+
+
+def _lifecycle(rt):
+    m = rt.metrics_summary()
+    return (rt.iteration, m["output_tokens"], m["preemptions"], m["repeated_kv_tokens"], m["prefill_tokens"],
+            m["decode_tokens"])
+
+
+@pytest.mark.parametrize("case", FORCED, ids=_ids)
+def test_forced_recompute_preemption_reference_cpu(case):
+    torch.set_num_threads(1)
+    tokens, rt = run_c1(case, "cpu", "reference", policy="recompute", kv_factor=0.5)
+    summary = rt.metrics_summary()
+    assert (summary["preemptions"], summary["repeated_kv_tokens"]) == (1, 16)
+    assert tokens == case["outputs"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", FORCED, ids=_ids)
+def test_forced_recompute_preemption_both_backends_gpu(case):
+    """Reference and HIP decode backends on the GPU: one preemption, 16
+    replayed KV tokens, identical tokens and lifecycle counts."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    out = {}
+    for backend in ("reference", "hip"):
+        print(f"  C1 forced preemption {backend} {_ids(case)}", flush=True)
+        tokens, rt = run_c1(case, "cuda", backend, policy="recompute", kv_factor=0.5)
+        out[backend] = (tokens, _lifecycle(rt))
+    assert out["hip"] == out["reference"]
+    assert out["hip"][1][2:4] == (1, 16)
+    assert out["hip"][0] == case["outputs"]
