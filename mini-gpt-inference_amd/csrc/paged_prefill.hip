@@ -643,13 +643,22 @@ template <> struct TrRead<f16_t> {
 };
 
 // One 16-byte copy per lane from global memory into LDS at lds_base + 16 *
-// lane (lds_base wave-uniform, through M0): from a per-lane address, or from a
-// wave-uniform base plus a per-lane 32-bit offset.
+// lane (lds_base wave-uniform): global_load_lds_dwordx4 from a per-lane
+// address, or from a wave-uniform base plus a per-lane 32-bit offset. The
+// instruction takes its LDS base from M0; the "{m0}" operand has the compiler
+// set M0 to lds_base before the statement (the asm only reads it), and the
+// s_nop is the wait state an LDS copy needs after an SALU write of M0. The
+// copy stays opaque to the compiler's wait-count tracking: the pipeline below
+// counts its copies itself (wait_and_barrier). With the compiler's own
+// __builtin_amdgcn_global_load_lds the kernel measured 4% slower on MI355X
+// (2048 rows after 2048: 70.5-71.1 against 67.8-68.0 us on one box), as the
+// compiler then drains every LDS read (lgkmcnt(0)) before MFMAs that use
+// them.
 __device__ __forceinline__ void copy16_to_lds(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
 }
 __device__ __forceinline__ void copy16_to_lds(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base)
                : "memory");
 }
 

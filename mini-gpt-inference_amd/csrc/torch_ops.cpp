@@ -63,6 +63,7 @@ void kv_append(const at::Tensor& kp, const at::Tensor& vp, int64_t layer_idx, co
   if (k.dim() != 3 || v.sizes() != k.sizes()) value_error("k and v must have matching shape [T,H,D]");
   check_pool(kp, vp);
   const int64_t T = k.size(0), L = kp.size(0), N = kp.size(1), S = kp.size(2), H = kp.size(3), D = kp.size(4);
+  if (S <= 0) value_error("block_size must be positive");
   if (k.size(1) != H || k.size(2) != D) value_error("k/v head dimensions do not match the KV pool");
   const int pd = dtype_code(kp.scalar_type());
   if (pd < 0 || vp.scalar_type() != kp.scalar_type()) value_error("KV pool must be float32, bfloat16 or float16");
@@ -137,6 +138,7 @@ at::Tensor paged_prefill(const at::Tensor& q, const at::Tensor& kp, const at::Te
     value_error("KV pool dtype must match q dtype");
   check_pool(kp, vp);
   const int64_t L = kp.size(0), N = kp.size(1), S = kp.size(2);
+  if (S <= 0) value_error("block_size must be positive");
   if (kp.size(3) != h || kp.size(4) != d) value_error("KV head dimensions do not match q");
   const int bti = index_code(bt.scalar_type());
   if (bt.dim() != 1 || bti < 0) value_error("block_table must be a 1-D integer tensor");

@@ -113,6 +113,8 @@ SPLIT_CASES = [
     (100, 20, 4, 256, 16, 64),
     (64, 64, 8, 32, 16, 64),
     (77, 150, 3, 128, 5, 128),
+    (300, 100, 4, 96, 16, 64),
+    (250, 90, 2, 48, 16, 128),
 ]
 
 
@@ -137,7 +139,8 @@ def test_forced_key_split_matches_oracle(monkeypatch, start, T, H, D, S, keys, d
 # MINIVLLM_HIP_PREFILL_TR: 0 is paged_prefill_mfma; the others are
 # paged_prefill_tr's (groups - 1, wavefronts per group, 16-row blocks per
 # wavefront, tiles in flight). Cases: block sizes 16 .. 256 (one to sixteen
-# 16-key granules per block), head dims 64 and 128, partial tiles, and
+# 16-key granules per block), head dims 48 to 128 (below and at the
+# kernels' padded widths of 64 and 128), partial tiles, and
 # contexts past 16384 keys, where the workgroup's block-table window moves.
 TR_CONFIGS = ["0", "412", "422", "812", "1412", "1422"]
 TR_CASES = [
@@ -149,6 +152,11 @@ TR_CASES = [
     (5, 300, 2, 128, 256),
     (16200, 300, 2, 128, 16),
     (16300, 200, 1, 64, 16),
+    # head dims below the kernel's padded width (96 and 80 in the 128-wide
+    # kernels, 48 in the 64-wide ones): the chunks past D read zeros
+    (100, 130, 4, 96, 16),
+    (63, 65, 4, 80, 32),
+    (200, 150, 2, 48, 16),
 ]
 _TR_EXPECTED: dict = {}
 
@@ -236,6 +244,20 @@ def test_invalid_table_entries_are_masked(monkeypatch, dtype, split_keys):
     out0 = run_hip(q, pool, first, 0, layer)
     check(out0, q, pool, first, 0, layer)
     assert torch.count_nonzero(out0[:16]) == 0
+
+
+def test_zero_block_size_pool_is_refused():
+    """A pool whose blocks hold no tokens is refused on the host, before any launch."""
+    pool = KVBlockPool(1, 4, 0, 2, 64, device=DEV, dtype=torch.bfloat16)
+    q = torch.zeros((3, 2, 64), device=DEV, dtype=torch.bfloat16)
+    table = torch.zeros(4, dtype=torch.long, device=DEV)
+    with pytest.raises(ValueError, match="block_size must be positive"):
+        hpd.paged_prefill_hip(q, pool, table, 0, 0)
+    with pytest.raises(ValueError, match="block_size must be positive"):
+        hpd.kv_append(pool, 0, q, q, torch.zeros(3, dtype=torch.long, device=DEV))
+    with pytest.raises(ValueError, match="block_size must be positive"):
+        hpd.paged_attention_batch_hip(q, pool, table.view(3 + 1, 1)[:3], torch.ones(3, dtype=torch.long,
+                                                                                   device=DEV), 0)
 
 
 def test_int32_table_and_contiguous_q_match_int64_and_view():
