@@ -121,30 +121,48 @@ def lib() -> ctypes.CDLL:
 
 
 def ops():
-    """The PyTorch binding (_hip_ops: kv_append, paged_decode, paged_prefill
-    on tensors, validated in C++, calling the C ABI on the current stream).
-    Raises RuntimeError when it is unavailable."""
+    """The eager path's binding: kv_append, paged_decode and paged_prefill on
+    tensors, validated, calling the C ABI on the current stream.
+
+    Normally the PyTorch extension _hip_ops (csrc/torch_ops.cpp). When the
+    library loads but the extension does not (missing, or built against
+    another PyTorch), the same calls go through ctypes (minivllm._ctypes_ops:
+    same checks and messages, same kernels and bits, more host time per
+    call), with a warning. Raises RuntimeError when the library itself is
+    unavailable."""
     global _ops
     if _ops is not None:
         return _ops
     lib()  # the library first: a clear error when it is the missing piece
     with _lock:
         if _ops is None:
-            import importlib.util
-
-            path = ops_path()
-            if not path.exists():
-                raise RuntimeError(
-                    f"HIP extension not built: {path} is missing "
-                    "(run `python -c 'import __graft_entry__ as g; g.build()'` at the repo root)")
             try:
-                spec = importlib.util.spec_from_file_location("minivllm._hip_ops", path)
-                mod = importlib.util.module_from_spec(spec)
-                spec.loader.exec_module(mod)
-            except (ImportError, OSError) as exc:
-                raise RuntimeError(f"HIP extension failed to load: {exc}") from exc
-            _ops = mod
+                _ops = _load_extension()
+            except RuntimeError as exc:
+                import warnings
+
+                from . import _ctypes_ops
+
+                warnings.warn(f"{exc}; calling libminivllm_hip.so through ctypes instead", RuntimeWarning,
+                              stacklevel=2)
+                _ops = _ctypes_ops
     return _ops
+
+
+def _load_extension():
+    """Imports the _hip_ops extension module; RuntimeError when it cannot."""
+    import importlib.util
+
+    path = ops_path()
+    if not path.exists():
+        raise RuntimeError(f"PyTorch binding not built: {path} is missing")
+    try:
+        spec = importlib.util.spec_from_file_location("minivllm._hip_ops", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+    except (ImportError, OSError) as exc:
+        raise RuntimeError(f"PyTorch binding failed to load: {exc}") from exc
+    return mod
 
 
 @functools.lru_cache(maxsize=1024)

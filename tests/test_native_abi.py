@@ -53,6 +53,39 @@ def test_torch_binding_loads_and_validates_on_the_host():
         hpd.paged_prefill_hip(q, pool, torch.zeros(1, dtype=torch.long), 0, 0)
 
 
+def test_ctypes_path_when_the_extension_cannot_load(monkeypatch, tmp_path):
+    """With the library present but the _hip_ops extension missing, the eager
+    calls go through ctypes (minivllm._ctypes_ops), with a warning, and
+    refuse CPU tensors with the extension's messages."""
+    from minivllm import _ctypes_ops
+    from minivllm import hip_paged_decode as hpd
+    from minivllm.kv_block_pool import KVBlockPool
+
+    monkeypatch.setattr(_native, "_ops", None)
+    monkeypatch.setattr(_native, "ops_path", lambda: tmp_path / "_hip_ops_missing.so")
+    with pytest.warns(RuntimeWarning, match="through ctypes"):
+        assert _native.ops() is _ctypes_ops
+    assert _native.ops() is _ctypes_ops  # chosen once
+    pool = KVBlockPool(1, 4, 16, 2, 64)
+    q = torch.zeros(1, 2, 64)
+    with pytest.raises(ValueError, match="^q must be on a GPU device for the HIP backend$"):
+        hpd.paged_attention_batch_hip(q, pool, torch.zeros(1, 1, dtype=torch.long),
+                                      torch.ones(1, dtype=torch.long), 0)
+    with pytest.raises(ValueError, match="^KV pool must be on a GPU device for the HIP backend$"):
+        hpd.kv_append(pool, 0, q, q, torch.zeros(1, dtype=torch.long))
+    with pytest.raises(ValueError, match="^q must be on a GPU device for the HIP backend$"):
+        hpd.paged_prefill_hip(q, pool, torch.zeros(1, dtype=torch.long), 0, 0)
+
+
+def test_missing_library_is_an_error_not_a_fallback(monkeypatch, tmp_path):
+    """Without libminivllm_hip.so there is no path at all: RuntimeError."""
+    monkeypatch.setattr(_native, "_ops", None)
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "library_path", lambda: tmp_path / "libminivllm_hip_missing.so")
+    with pytest.raises(RuntimeError, match="HIP extension not built"):
+        _native.ops()
+
+
 def test_split_tokens_and_workspace_sizes():
     lib = _native.lib()
     # decode microbench shape: M = 256 columns of S = 16 -> 8 partitions of 512
