@@ -415,6 +415,10 @@ def e2e_lockstep_line(dev, fp32_reference: bool = False):
            "max_logit_abs": st["max_logit_abs"], "max_logit_fraction_of_bound": round(st["max_logit_ratio"], 3),
            "max_kv_abs": st["max_kv_abs"], "max_kv_fraction_of_bound": round(st["max_kv_ratio"], 3),
            "preemptions": st["preemptions"], "recomputed_sequences": len(st["recomputed_seqs"]),
+           "reference_runtime_s": round(ls.wall["reference"], 2), "hip_runtime_s": round(ls.wall["hip"], 2),
+           "same_gpu_speedup": round(ls.wall["reference"] / ls.wall["hip"], 2) if ls.wall["hip"] else None,
+           "runtime_time_note": "seconds inside each runtime's steps over the same schedule (sdpa_v2 prefill "
+                                "in both; device-synchronised per step, checks excluded)",
            "wall_s": round(time.perf_counter() - t0, 1),
            "criterion": f"logits and decode-written KV within {atol:g} + {rtol:g}*max|ref row|; layer-0 and "
                         "prefill-written KV bit-identical; a token may differ only at a reference top-2 "

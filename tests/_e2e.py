@@ -391,6 +391,9 @@ class Lockstep:
         self.ref = _Probe(*make_runtime(spec, model, prompts, device, dtype))
         self.hip = _Probe(*make_runtime(spec, model, prompts, device, dtype))
         self.forced: list[tuple[int, str, int, float]] = []   # (step, seq_id, token index, ref margin)
+        # Seconds inside each runtime's steps (device-synchronised at both
+        # ends of every step; the checks between steps are not counted).
+        self.wall = {"reference": 0.0, "hip": 0.0}
         # max_*_ratio: the largest deviation as a fraction of its bound (<= 1 passes).
         self.stats = {"steps": 0, "decode_rows": 0, "decode_rows_checked": 0, "max_logit_abs": 0.0,
                       "max_logit_ratio": 0.0, "kv_tokens_checked": 0, "kv_exact_tokens": 0, "max_kv_abs": 0.0,
@@ -419,10 +422,18 @@ class Lockstep:
 
     def step(self) -> None:
         step = self.stats["steps"] + 1
+        sync = torch.cuda.synchronize if self.model.language_model_head.weight.is_cuda else (lambda: None)
+        sync()
+        t0 = time.perf_counter()
         self.model.set_decode_attention_backend("reference")
         self._step_reference()
+        sync()
+        t1 = time.perf_counter()
         self.model.set_decode_attention_backend("hip")
         self.hip.step()
+        sync()
+        self.wall["reference"] += t1 - t0
+        self.wall["hip"] += time.perf_counter() - t1
         self.stats["steps"] = step
         a, b = self.ref, self.hip
         if a.plan != b.plan:

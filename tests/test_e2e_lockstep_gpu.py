@@ -77,7 +77,8 @@ def _run_full(progress, criterion: dict, ref_attention=None) -> _e2e.Lockstep:
     progress("  " + _report(ls, t0))
     margins = collections.Counter(round(m, 6) for *_, m in ls.forced)
     progress(f"  streams never forced: {len(ls.ref.seqs) - len(ls.forced_streams)}/{len(ls.ref.seqs)}; "
-             f"forced-tie margins: {dict(sorted(margins.items()))}")
+             f"forced-tie margins: {dict(sorted(margins.items()))}; seconds in steps: reference "
+             f"{ls.wall['reference']:.1f}, hip {ls.wall['hip']:.1f}")
     ls.finish_checks()
     assert ls.stats["preemptions"] > 0, "the run must reach recompute preemption"
     assert ls.stats["recomputed_seqs"], "the run must reach a recompute prefill"
