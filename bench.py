@@ -20,15 +20,20 @@ contexts, the small end-to-end model and a window of the full runtime.
 
 Extras (skipped with --no-extras) time other decode shapes, the KV append,
 the KV append plus decode attention of one high-batch step on one pool, the
-paged prefill kernel and same-GPU comparisons with the PyTorch backends.
-The end-to-end block (skipped with --no-e2e) runs the full runtime under
-recompute preemption and puts its decode tokens/s (generated tokens / wall
-seconds) in `end_to_end`, then runs it to completion in lock step against
-the PyTorch reference decode backend (skipped with --no-lockstep).
+paged prefill kernel, attention-only speedups against the PyTorch online_v1
+and the small-model end-to-end A/B against the PyTorch reference backend
+(the reference's method: 2 warm-ups and 7 alternating repeats, with and
+without forced recompute preemption). The end-to-end block (skipped with
+--no-e2e) runs the full runtime under recompute preemption and puts its
+decode tokens/s (generated tokens / wall seconds) in `end_to_end`, then runs
+it to completion in lock step against the PyTorch reference decode backend
+(skipped with --no-lockstep; --lockstep-fp32 adds a second run against
+online_v1 on float32 copies), checking every decode row.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--dtype bf16|fp32]
                        [--split-tokens P] [--no-extras] [--no-cpu-baseline]
-                       [--no-e2e] [--e2e-requests R] [--prefill]
+                       [--no-e2e] [--e2e-requests R] [--no-lockstep]
+                       [--lockstep-fp32] [--prefill]
 """
 from __future__ import annotations
 
