@@ -839,6 +839,8 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   const bool all_dims = a.D == DP;
   const int kbuf0 = grp * STAGES, vbuf0 = grp * STAGES;  // this group's first K and V buffers
 
+  const uint32_t k_dst0 = lds_addr(k_lds) + wave * (GPW * 1024);  // this wave's copy destinations
+  const uint32_t v_dst0 = lds_addr(v_lds) + wave * (GPW * 1024);
   // The copies of one tile by this wave: per granule j its K and V
   // sources, whether every row is a key (the scalar-base form), and the
   // destinations.
@@ -860,8 +862,8 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
     cp.kt0 = key0 + t * kTileKeys;
     const uint32_t valid = ((uint32_t)__builtin_amdgcn_ballot_w64(gv >= 0) >> (4 * tg)) & 0xfu;  // granule j valid
     cp.fast = all_dims && cp.kt0 + kTileKeys <= kv_end && valid == 0xfu;
-    cp.kdst = lds_addr(k_lds) + (tg * STAGES + KS) * TILEB + wave * (GPW * 1024);
-    cp.vdst = lds_addr(v_lds) + (tg * STAGES + VS) * TILEB + wave * (GPW * 1024);
+    cp.kdst = (tg * STAGES + KS) * TILEB;  // offsets from this wave's LDS bases (k_dst0, v_dst0)
+    cp.vdst = (tg * STAGES + VS) * TILEB;
     const int gw0 = 4 * tg + ((wave * RW) >> 4);
 #pragma unroll
     for (int j = 0; j < GRW; ++j) {
@@ -877,20 +879,29 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       if (cp.live && ((valid >> j) & 1u)) vm |= 0xffffull << (16 * j);
     return cp;
   };
-  // Issues copy i (one K and one V row group) of a plan.
+  // Issues copy i (one K and one V row group) of a plan. The LDS
+  // destination is formed at the copy from this wave's two bases, passed
+  // through an empty asm so the compiler cannot hoist every base + offset
+  // sum out of the loop: held in scalar registers, those sums (one per
+  // copy, stage and group) ran past the register file and were spilled to
+  // vector-register lanes, a v_readlane per copy.
   auto copy_one = [&](const CopyPlan& cp, int i) __attribute__((always_inline)) {
     if (!cp.live) return;
     const int j = i / CPGW;
+    uint32_t kd = k_dst0, vd = v_dst0;
+    asm volatile("" : "+s"(kd), "+s"(vd));
+    kd += cp.kdst + i * 1024;
+    vd += cp.vdst + i * 1024;
     if (cp.fast) {
-      copy16_to_lds(cp.kb[j], koff[i], cp.kdst + i * 1024);
-      copy16_to_lds(cp.vb[j], voff[i], cp.vdst + i * 1024);
+      copy16_to_lds(cp.kb[j], koff[i], kd);
+      copy16_to_lds(cp.vb[j], voff[i], vd);
     } else {
       const bool ok = cp.G[j] >= 0 && cp.kt0 + copy_row(i) < kv_end;
       const int ck = k_chunk(i), cv = v_chunk(i);
       const unsigned char* ks = (ok && ck * 8 < a.D) ? cp.kb[j] + koff[i] : kZeroRow + ck * 16;
       const unsigned char* vs = (ok && cv * 8 < a.D) ? cp.vb[j] + voff[i] : kZeroRow + cv * 16;
-      copy16_to_lds(ks, cp.kdst + i * 1024);
-      copy16_to_lds(vs, cp.vdst + i * 1024);
+      copy16_to_lds(ks, kd);
+      copy16_to_lds(vs, vd);
     }
   };
   auto copy_all = [&](const CopyPlan& cp) __attribute__((always_inline)) {
