@@ -78,6 +78,25 @@ def test_dense_matches_online_for_ragged_blocks(bs, context):
     assert np.isfinite(dense).all()
 
 
+@pytest.mark.parametrize("batch,length", [(1, 1), (1, 15), (1, 16), (2, 17), (4, 33), (4, 64), (4, 65),
+                                          (2, 128), (4, 129), (2, 256), (4, 257)])
+def test_online_matches_torch_softmax_on_the_fused_decode_grid(batch, length):
+    """The correctness grid of experiments/gpu_day6_fused_decode_ab.py:171-181
+    (8 heads, head_dim 32, block 16, seed 20261030 + B + L): the oracle's
+    online recurrence against torch.softmax over each row's gathered tokens
+    (float64), the library routine the reference's dense_gold uses."""
+    q, pool, tables, lens, layer = fx.build_case(batch, length, 8, 32, 16, "mixed", seed=20261030 + batch + length)
+    k, v = np_pool(pool)
+    online = ora.paged_attention_online_v1(q.numpy(), k, v, tables.numpy(), lens.numpy(), layer)
+    for b in range(batch):
+        n = int(lens[b])
+        blocks = tables[b, :-(-n // 16)]
+        keys = pool.k[layer, blocks].reshape(-1, 8, 32)[:n].double()
+        vals = pool.v[layer, blocks].reshape(-1, 8, 32)[:n].double()
+        w = torch.softmax(torch.einsum("hd,thd->ht", q[b].double(), keys) / 32 ** 0.5, dim=-1)
+        np.testing.assert_allclose(online[b], torch.einsum("ht,thd->hd", w, vals).numpy(), rtol=1e-9, atol=1e-9)
+
+
 def test_build_case_has_nontrivial_mapping_nan_padding_and_strided_q():
     q, pool, tables, lens, layer = fx.build_case(4, 65, 8, 32, 16, "mixed")
     assert tables.shape[0] == 4 and bool((tables == -1).any())

@@ -81,6 +81,19 @@ def test_kernel_matches_oracle_reference_grid(bs, length, batch, dim):
     np.testing.assert_allclose(got, ora.dense_gold(*oracle_args(q, pool, tables, lens, layer)), **F32_TOL)
 
 
+@pytest.mark.parametrize("batch,length", [(1, 1), (1, 15), (1, 16), (2, 17), (4, 33), (4, 64), (4, 65),
+                                          (2, 128), (4, 129), (2, 256), (4, 257)])
+def test_kernel_matches_reference_fused_decode_grid(batch, length):
+    """The correctness grid of experiments/gpu_day6_fused_decode_ab.py:171-181
+    (8 heads, head_dim 32, block 16, mixed lengths, seed 20261030 + B + L)
+    against the dense closed form, at that script's 2e-4 and at 1e-5."""
+    q, pool, tables, lens, layer = fx.build_case(batch, length, 8, 32, 16, "mixed", seed=20261030 + batch + length)
+    got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
+    want = ora.dense_gold(*oracle_args(q, pool, tables, lens, layer))
+    np.testing.assert_allclose(got, want, rtol=2e-4, atol=2e-4)
+    np.testing.assert_allclose(got, want, **F32_TOL)
+
+
 def test_large_logits_stable():
     q, pool, tables, lens, layer = fx.build_case(2, 65, 4, 32, 16, "mixed", scale=8.0)
     got = hip(q, fx.pool_to_device(pool, DEV), tables, lens, layer)
