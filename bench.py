@@ -10,8 +10,9 @@ algorithmic bytes are
   sum_b ctx_b*H*D*e*2 + B*H*D*(e_q + e_out) + sum_b ceil(ctx_b/S)*e_idx + B*e_idx
 (valid tokens only; partial-block padding, split partials and the merge pass
 are overhead). Time per step is the median of K per-call HIP event pairs on
-torch's current stream (the stream the kernels launch on), after W untimed
-calls, the region bracketed by device synchronisations. `cpu_baseline`
+torch's current stream (the stream the kernels launch on), after about
+50 ms of untimed calls (the GPU's clocks settle under sustained load) and W
+untimed calls, the region bracketed by device synchronisations. `cpu_baseline`
 times the C restatement of the reference's online-softmax decode
 (oracle/paged_decode_oracle.c, fp32 accumulation) on this host's cores over
 the same workload, with rows for the package's PyTorch online_v1 on the CPU
@@ -66,8 +67,9 @@ def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # 200 untimed calls (about 80 ms of the headline call) let the GPU's clocks
-    # settle: the median read 82.85-82.89 % after 200, 82.68-82.70 % after 10.
+    # Untimed calls after the ~50 ms clock-settle phase every decode line runs;
+    # with that phase the median no longer depends on this count (the median
+    # read 82.68-82.70 % after 10 calls and no settle phase, 82.85-82.89 % after 200).
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--dtype", choices=("bf16", "fp32"), default="bf16")
     ap.add_argument("--split-tokens", type=int, default=0)
@@ -168,11 +170,14 @@ def time_calls(fn, steps: int, warmup: int) -> dict:
 
 def decode_line(w, steps, warmup, split):
     """One decode-attention call per step; the rate is algorithmic bytes over
-    the median of the per-call event timings."""
+    the median of the per-call event timings. About 50 ms of untimed calls
+    run first so the GPU's clocks settle (as for the prefill lines), then
+    `warmup` untimed calls, then the `steps` timed ones."""
     from minivllm import hip_paged_decode as hpd
 
     fn = lambda: hpd.paged_attention_batch_hip(w.q, w.pool, w.tables, w.ctx, w.layer,  # noqa: E731
                                                split_tokens=split)
+    warm_up(fn)
     t = time_calls(fn, steps, warmup)
     ms = t["median_ms"]
     nbytes = w.algorithmic_bytes()
