@@ -699,12 +699,21 @@ __device__ __forceinline__ void static_for(F&& f) {
 // the copies of both groups' tiles. A wavefront can then own 32 query rows
 // (each K and V read from LDS feeds two products) while two wavefronts share
 // every SIMD.
-template <typename T, int DP, int WAVES, int QPW, int STAGES, int GROUPS>
+//
+// PAIRED (QPW = 2) balances the causal triangle: the chunk's rows are cut
+// into half tiles of 16 WAVES rows, and the workgroup for pair p takes half
+// tiles p and nh - 1 - p (nh half tiles), a wavefront's block 0 in the first
+// and block 1 in the second. Every pair then holds about the same number of
+// (row block, key tile) products, where plain 2-block tiles range from the
+// chunk's shortest chain to its longest and the longest sets the kernel's
+// time. Key tiles past block 0's last row run block 1 alone.
+template <typename T, int DP, int WAVES, int QPW, int STAGES, int GROUPS, bool PAIRED = false>
 __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const PrefillArgs a) {
   static_assert(sizeof(T) == 2 && (DP == 64 || DP == 128), "2-byte types, head dim 64 or 128");
   static_assert(WAVES == 2 || WAVES == 4 || WAVES == 8, "two, four or eight wavefronts per group");
   static_assert(STAGES >= 2 && STAGES <= 4, "two to four tiles in flight");
   static_assert(GROUPS == 1 || GROUPS == 2, "one or two groups");
+  static_assert(!PAIRED || QPW == 2, "paired rows take two 16-row blocks per wavefront");
   constexpr int ROWB = DP * 2;               // bytes per key row
   constexpr int CPR = DP / 8;                // 16-byte chunks per key row
   constexpr int TILEB = kTileKeys * ROWB;    // bytes per K (or V) tile
@@ -728,8 +737,11 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   __shared__ __align__(1024) unsigned char v_lds[VBUFS * TILEB];
   __shared__ __align__(16) int gran[kGranuleWindow];
 
-  // Grid mapping: as paged_prefill_mfma.
-  const int nq = (a.T + QB - 1) / QB;
+  // Grid mapping: as paged_prefill_mfma (PAIRED: one workgroup per pair of
+  // half tiles and head).
+  constexpr int HB = 16 * WAVES;  // PAIRED: rows per half tile
+  const int nh = (a.T + HB - 1) / HB;
+  const int nq = PAIRED ? (nh + 1) / 2 : (a.T + QB - 1) / QB;
   const int wg = (int)blockIdx.x;
   int h, qr;
   if ((a.H & 7) == 0) {
@@ -751,24 +763,45 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   const int grp = GROUPS == 1 ? 0 : wall / WAVES;  // group of this wavefront
   const int wave = GROUPS == 1 ? wall : wall % WAVES;  // wavefront within its group
   const int col = lane & 15, g = lane >> 4;
-  const int qw0 = qt * QB + wave * 16 * QPW;
-  const int kv_end = a.start + min(a.T, (qt + 1) * QB);
+  // First chunk row of each of this wavefront's 16-row blocks (>= a.T: the
+  // block has no rows) and the chunk rows this workgroup's keys reach.
+  int rb[QPW], kv_rows;
+  if constexpr (PAIRED) {
+    const int hs = qt, hl = nh - 1 - qt;  // the middle half tile of an odd nh runs as block 1 alone
+    rb[0] = hs < hl ? hs * HB + wave * 16 : a.T;
+    rb[1] = hl * HB + wave * 16;
+    kv_rows = (hl + 1) * HB;
+  } else {
+#pragma unroll
+    for (int b = 0; b < QPW; ++b) rb[b] = qt * QB + wave * 16 * QPW + 16 * b;
+    kv_rows = (qt + 1) * QB;
+  }
+  const int kv_end = a.start + min(a.T, kv_rows);
   const int part = (int)blockIdx.y;
   const int ntiles_all = (kv_end + kTileKeys - 1) / kTileKeys;
   const int tpp = a.part_keys > 0 ? a.part_keys / kTileKeys : ntiles_all;
   const int tb = part * tpp;
   if (tb >= ntiles_all) return;  // uniform: this query tile needs fewer partitions
   const int key0 = tb * kTileKeys;
-  const bool wave_active = qw0 < a.T;
-  const int wave_first = a.start + qw0;
-  const int wave_last = a.start + min(a.T, qw0 + 16 * QPW) - 1;
+  // Absolute positions of each block's first and last rows; the wavefront's
+  // last position over the blocks that have rows (-1: none).
+  int blk_first[QPW], blk_last[QPW];
+  int wave_last = -1;
+#pragma unroll
+  for (int b = 0; b < QPW; ++b) {
+    blk_first[b] = a.start + rb[b];
+    blk_last[b] = a.start + min(a.T, rb[b] + 16) - 1;
+    if (rb[b] < a.T) wave_last = max(wave_last, blk_last[b]);
+  }
+  const bool wave_active = wave_last >= 0;
+  const int wave_first = blk_first[0];
   const int ntiles = min(ntiles_all, tb + tpp) - tb;
   const int nsteps = (ntiles + GROUPS - 1) / GROUPS;  // loop steps (every group takes them all)
   const int ntg = (ntiles - grp + GROUPS - 1) / GROUPS;  // tiles of this wave's group
   int qi[QPW], qpos[QPW];
 #pragma unroll
   for (int b = 0; b < QPW; ++b) {
-    qi[b] = qw0 + 16 * b + col;
+    qi[b] = rb[b] + col;
     qpos[b] = a.start + (qi[b] < a.T ? qi[b] : a.T - 1);
   }
 
@@ -949,8 +982,10 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   const float cs = query_scale(a.scale_log2);  // the query carries the sign (query_sign)
   const float inv_cs = 1.f / cs;
 
-  // QK^T and softmax of the tile in stage ST: packs P for the PV product.
-  auto qk_softmax = [&](int kt0, uint64_t vm, int ST, uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
+  // QK^T and softmax of the tile in stage ST for the blocks in the mask
+  // (bit b: block b; a Stage<mask> tag): packs P for the PV product.
+  auto qk_softmax = [&](auto bm, int kt0, uint64_t vm, int ST, uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
+    constexpr int BM = decltype(bm)::value;
     const unsigned char* kl = k_lds + ST * TILEB;
     // ---- S^T blocks: lane holds keys 32c + 8g + 4hh + i (kb = 2c + hh) of
     // query column `col` of each 16-row block b. Block kb + 1's K reads go
@@ -971,14 +1006,18 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
 #pragma unroll
       for (int f = 0; f < NQF; ++f)
 #pragma unroll
-        for (int b = 0; b < QPW; ++b) s[b][kb] = MM::mfma(kv[kb & 1][f], qf[b][f], s[b][kb]);
+        for (int b = 0; b < QPW; ++b)
+          if ((BM >> b) & 1) s[b][kb] = MM::mfma(kv[kb & 1][f], qf[b][f], s[b][kb]);
       __builtin_amdgcn_sched_barrier(0);
     }
 
     // ---- masks (causal, invalid granules), online softmax, P packed for PV
-    const bool full = kt0 + kTileKeys - 1 <= wave_first && vm == ~0ull;
+    const bool full_wave = kt0 + kTileKeys - 1 <= wave_first && vm == ~0ull;
 #pragma unroll
     for (int b = 0; b < QPW; ++b) {
+      if (!((BM >> b) & 1)) continue;
+      // PAIRED blocks lie apart, so each block tests its own first row.
+      const bool full = PAIRED ? kt0 + kTileKeys - 1 <= blk_first[b] && vm == ~0ull : full_wave;
       float p[4][4];
       if (full) {
 #pragma unroll
@@ -1029,7 +1068,8 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   };
   // O^T += V^T P^T (and the row sums) for the tile in stage ST, per 32-key
   // slice c; each V read feeds QPW products.
-  auto pv = [&](int ST, const uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
+  auto pv = [&](auto bm, int ST, const uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
+    constexpr int BM = decltype(bm)::value;
     const unsigned char* vl = v_lds + ST * TILEB;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -1043,9 +1083,11 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int b = 0; b < QPW; ++b) oacc[b][db] = MM::mfma(vv[db], pb[b][c], oacc[b][db]);
+        for (int b = 0; b < QPW; ++b)
+          if ((BM >> b) & 1) oacc[b][db] = MM::mfma(vv[db], pb[b][c], oacc[b][db]);
 #pragma unroll
-      for (int b = 0; b < QPW; ++b) lacc[b] = MM::mfma(ones, pb[b][c], lacc[b]);
+      for (int b = 0; b < QPW; ++b)
+        if ((BM >> b) & 1) lacc[b] = MM::mfma(ones, pb[b][c], lacc[b]);
       __builtin_amdgcn_sched_barrier(0);  // slice 1's V reads wait for slice 0's products
     }
   };
@@ -1092,26 +1134,46 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       if (SI + 1 < nsteps) e = tile_granules(SI + 1);
     }
   });
-  for (int u0 = 0; u0 < nsteps; u0 += STAGES) {
-    static_for<0, STAGES>([&](auto sc) {
-      constexpr int SI = decltype(sc)::value;
-      constexpr int SN = (SI + STAGES - 1) % STAGES;  // buffers of step u + STAGES - 1
-      const int u = u0 + SI;
-      if (u >= nsteps) return;
-      wait_step(u);
-      const int un = u + STAGES - 1;
-      if (un < nsteps) {
-        issue_step(un, e, SN, vm[SN]);
-        if (un + 1 < nsteps) e = tile_granules(un + 1);
-      }
-      const int kt0 = key0 + (u * GROUPS + grp) * kTileKeys;
-      if (u < ntg && wave_active && kt0 <= wave_last) {
-        uint4 pb[QPW][2];
-        qk_softmax(kt0, vm[SI], SI, pb);
-        pv(SI, pb);
-      }
-    });
+  // Steps [u_lo, u_hi) with the blocks of mask bm (a Stage<mask> tag).
+  auto run_steps = [&](auto bm, int u_lo, int u_hi) __attribute__((always_inline)) {
+    for (int u0 = u_lo - u_lo % STAGES; u0 < u_hi; u0 += STAGES) {
+      static_for<0, STAGES>([&](auto sc) {
+        constexpr int SI = decltype(sc)::value;
+        constexpr int SN = (SI + STAGES - 1) % STAGES;  // buffers of step u + STAGES - 1
+        const int u = u0 + SI;
+        if (u < u_lo || u >= u_hi) return;
+        wait_step(u);
+        const int un = u + STAGES - 1;
+        if (un < nsteps) {
+          issue_step(un, e, SN, vm[SN]);
+          if (un + 1 < nsteps) e = tile_granules(un + 1);
+        }
+        const int kt0 = key0 + (u * GROUPS + grp) * kTileKeys;
+        if (u < ntg && wave_active && kt0 <= wave_last) {
+          uint4 pb[QPW][2];
+          qk_softmax(bm, kt0, vm[SI], SI, pb);
+          pv(bm, SI, pb);
+        }
+      });
+    }
+  };
+  if constexpr (PAIRED) {
+    // Block 0's rows come first. The steps whose tile (of this wavefront's
+    // group) reaches them run both blocks, the rest block 1 alone, in two
+    // loops: one loop with a branch between the two bodies made the compiler
+    // spill registers. Where block 1 has no rows, every step runs both (its
+    // rows past the chunk are computed and never stored).
+    int u_split = nsteps;
+    if (rb[1] < a.T) {
+      const int f = rb[0] < a.T ? (blk_last[0] - key0) / kTileKeys - grp : -1;
+      u_split = f >= 0 ? min(nsteps, f / GROUPS + 1) : 0;
+    }
+    run_steps(Stage<3>{}, 0, u_split);
+    run_steps(Stage<2>{}, u_split, nsteps);
+  } else {
+    run_steps(Stage<(1 << QPW) - 1>{}, 0, nsteps);
   }
+
 
   // ---- group 1 hands its state to group 0 through the drained tile
   // buffers: unnormalised outputs in the K buffers, (max, partial sum) in the
@@ -1210,12 +1272,13 @@ static bool tr_eligible(const PrefillArgs& a) {
   return (reinterpret_cast<uintptr_t>(a.k) % 16) == 0 && (reinterpret_cast<uintptr_t>(a.v) % 16) == 0;
 }
 
-template <typename T, int DP, int WAVES, int QPW, int STAGES, int GROUPS>
+template <typename T, int DP, int WAVES, int QPW, int STAGES, int GROUPS, bool PAIRED = false>
 hipError_t launch_tr_cfg(const PrefillArgs& a, hipStream_t stream) {
   constexpr int QB = 16 * QPW * WAVES;
+  constexpr int HB = 16 * WAVES;
   constexpr int NT = 64 * WAVES * GROUPS;
-  const int64_t wgs = ((int64_t)a.T + QB - 1) / QB * a.H;
-  const void* fn = reinterpret_cast<const void*>(&paged_prefill_tr<T, DP, WAVES, QPW, STAGES, GROUPS>);
+  const int64_t wgs = (PAIRED ? (((int64_t)a.T + HB - 1) / HB + 1) / 2 : ((int64_t)a.T + QB - 1) / QB) * a.H;
+  const void* fn = reinterpret_cast<const void*>(&paged_prefill_tr<T, DP, WAVES, QPW, STAGES, GROUPS, PAIRED>);
   static const int per_cu = resident_per_cu(fn, NT);
   PrefillArgs b = a;
   const bool split = a.part_keys > 0;
@@ -1223,15 +1286,15 @@ hipError_t launch_tr_cfg(const PrefillArgs& a, hipStream_t stream) {
                   wgs <= 2 * a.cus)
                      ? a.cus / 8 : 0;
   const dim3 grid((unsigned)wgs, split ? (unsigned)a.max_parts : 1u);
-  hipLaunchKernelGGL((paged_prefill_tr<T, DP, WAVES, QPW, STAGES, GROUPS>), grid, dim3(NT), 0, stream, b);
+  hipLaunchKernelGGL((paged_prefill_tr<T, DP, WAVES, QPW, STAGES, GROUPS, PAIRED>), grid, dim3(NT), 0, stream, b);
   return hipGetLastError();
 }
 
 // MINIVLLM_HIP_PREFILL_TR (read on every call) overrides the choice below for
 // tuning and tests: 0 takes paged_prefill_mfma; otherwise its decimal digits
-// set paged_prefill_tr's groups minus one (thousands), wavefronts per group,
-// 16-row query blocks per wavefront and tiles in flight per group (412, 422,
-// 812, 1412 or 1422). -1: unset.
+// set paged_prefill_tr's paired rows (ten thousands), groups minus one
+// (thousands), wavefronts per group, 16-row query blocks per wavefront and
+// tiles in flight per group (412, 422, 812, 1412, 1422 or 11422). -1: unset.
 int prefill_tr_mode() {
   const char* e = std::getenv("MINIVLLM_HIP_PREFILL_TR");
   return e && *e ? std::atoi(e) : -1;
@@ -1239,6 +1302,16 @@ int prefill_tr_mode() {
 
 // paged_prefill_tr configuration for a call, measured on MI355X (bf16,
 // D = 128, S = 16, 16 heads unless noted):
+//   * 11422 (1422 with paired rows: one workgroup per pair of 64-row half
+//     tiles) when those workgroups fill at least 7/8 of the CUs in one
+//     round: every workgroup then holds the same work. 2048 rows after
+//     2048: 68.2 against 71.1 us for 1422; at 0: 35.5 (1412: 38.0);
+//     after 512: 43.6 (1422: 47.6); after 4096 and 8192: 98.5 / 160.2
+//     (1422: 102.1 / 163.6); 8 heads, 4096 rows at 0: 58.0 (1412: 58.5,
+//     1422: 67.9), after 4096: 121.7 (1422: 130.7); 32 heads, 1024 rows
+//     at 0 and after 1024: 24.5 / 40.2 (412: 25.1, 1422: 42.0). A grid
+//     that fills 3/4 of the CUs leaves them idle all the same, and there
+//     the others win (1536 rows after 1536: 66.8 against 60.3 for 412);
 //   * 1422 (two groups of four 32-row wavefronts per 128-row query tile,
 //     one workgroup per CU): chunks after a prefix at least as long whose
 //     128-row tiles fill the CUs (2048 rows after 2048: 72-80 us; 412:
@@ -1250,7 +1323,9 @@ int prefill_tr_mode() {
 //   * 1412 (two groups of four 16-row wavefronts per 64-row tile): grids of
 //     64-row tiles that leave CUs empty, where splitting each workgroup's keys
 //     over two groups halves its serial chain (512 rows at 0: 13.5 us; 412:
-//     14.5);
+//     14.5), and first chunks (start 0) whose 64-row tiles take up to two
+//     rounds of the CUs (1536 rows: 26.8 against 31.3 for 412; 8 heads,
+//     3072 rows: 40.5 against 54.1);
 //   * 412 (two workgroups of four 16-row wavefronts per CU) otherwise, and
 //     whenever the keys are split over workgroups (its cost model assumes
 //     64-row tiles).
@@ -1258,10 +1333,12 @@ int prefill_tr_choice(const PrefillArgs& a) {
   const int forced = prefill_tr_mode();
   if (forced >= 0) return forced;
   const int64_t wgs128 = ((int64_t)a.T + 127) / 128 * a.H, wgs64 = ((int64_t)a.T + 63) / 64 * a.H;
+  const int64_t wgs_paired = (((int64_t)a.T + 63) / 64 + 1) / 2 * a.H;
   if (a.part_keys > 0) return 412;
+  if (wgs_paired <= a.cus && 8 * wgs_paired >= 7 * (int64_t)a.cus) return 11422;
   const int64_t mean_keys = (int64_t)a.start + a.T / 2;  // keys the mean query tile attends to
   if (wgs128 >= a.cus && (a.start >= a.T || (wgs128 > a.cus && mean_keys >= 20 * kTileKeys))) return 1422;
-  if (wgs64 <= a.cus) return 1412;
+  if (wgs64 <= a.cus || (a.start == 0 && wgs64 <= 2 * (int64_t)a.cus)) return 1412;
   return 412;
 }
 
@@ -1272,6 +1349,7 @@ hipError_t launch_tr(const PrefillArgs& a, int mode, hipStream_t stream) {
     case 812: return launch_tr_cfg<T, DP, 8, 1, 2, 1>(a, stream);
     case 1412: return launch_tr_cfg<T, DP, 4, 1, 2, 2>(a, stream);
     case 1422: return launch_tr_cfg<T, DP, 4, 2, 2, 2>(a, stream);
+    case 11422: return launch_tr_cfg<T, DP, 4, 2, 2, 2, true>(a, stream);
     default: return launch_tr_cfg<T, DP, 4, 1, 2, 1>(a, stream);  // 412
   }
 }

@@ -138,14 +138,17 @@ def test_forced_key_split_matches_oracle(monkeypatch, start, T, H, D, S, keys, d
 # Every configuration of the matrix-core prefill, selected through
 # MINIVLLM_HIP_PREFILL_TR: 0 is paged_prefill_mfma; the others are
 # paged_prefill_tr's (groups - 1, wavefronts per group, 16-row blocks per
-# wavefront, tiles in flight). Cases: block sizes 16 .. 256 (one to sixteen
-# 16-key granules per block), head dims 48 to 128 (below and at the
-# kernels' padded widths of 64 and 128), partial tiles, and
-# contexts past 16384 keys, where the workgroup's block-table window moves.
-TR_CONFIGS = ["0", "412", "422", "812", "1412", "1422"]
+# wavefront, tiles in flight; 11422 is 1422 with paired rows, each
+# workgroup taking a short and a long half tile). Cases: block sizes 16 ..
+# 256 (one to sixteen 16-key granules per block), head dims 48 to 128 (below
+# and at the kernels' padded widths of 64 and 128), partial tiles, odd and
+# even half-tile counts, and contexts past 16384 keys, where the workgroup's
+# block-table window moves.
+TR_CONFIGS = ["0", "412", "422", "812", "1412", "1422", "11422"]
 TR_CASES = [
     # start, T, H, D, S
     (0, 406, 8, 128, 16),
+    (300, 1000, 8, 128, 16),
     (1000, 200, 4, 128, 16),
     (63, 65, 4, 128, 32),
     (100, 130, 4, 64, 64),
@@ -183,6 +186,36 @@ def test_prefill_kernel_configs_match_oracle(monkeypatch, dtype, start, T, H, D,
     got = run_hip(q, pool, table, start, layer).float().cpu().numpy()
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got, want, **TOL[dtype])
+
+
+def test_paired_rows_automatic_choice_is_bit_identical_to_1422(monkeypatch):
+    """A 2048-row chunk after 2048 cached tokens with one head per 16 CUs:
+    the launcher takes the paired-row configuration, whose 64-row half-tile
+    pairs fill the chip in one round. Each row's 16-row block and key-tile
+    order are those of 1422, so the outputs are bit-identical to it; sampled
+    rows (the ends of half tiles included) are checked against the oracle."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus % 16 != 0:
+        pytest.skip("needs a CU count divisible by 16")
+    start, T, H, D, S = 2048, 2048, cus // 16, 128, 16
+    qkv, pool, table, layer = prefill_case(start, T, H, D, S, torch.bfloat16, seed=37, spare=1)
+    q = qkv.to(DEV)[:, 0]
+    monkeypatch.delenv("MINIVLLM_HIP_PREFILL_TR", raising=False)
+    auto = run_hip(q, pool, table, start, layer)
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_TR", "11422")
+    paired = run_hip(q, pool, table, start, layer)
+    monkeypatch.setenv("MINIVLLM_HIP_PREFILL_TR", "1422")
+    plain = run_hip(q, pool, table, start, layer)
+    assert torch.equal(auto, paired)
+    assert torch.equal(paired, plain)
+    rows = sorted({0, 15, 16, 63, 64, 1023, 1024, 1983, 1984, T - 1} |
+                  set(np.random.default_rng(5).integers(0, T, 22).tolist()))
+    kp, vp = fx.to_numpy(pool.k), fx.to_numpy(pool.v)
+    qn = fx.to_numpy(q)
+    got = paired.float().cpu().numpy()
+    for i in rows:
+        want = ora.paged_prefill(qn[i:i + 1], kp, vp, table.numpy(), start + i, layer)
+        np.testing.assert_allclose(got[i:i + 1], want, **BF16_TOL)
 
 
 @pytest.mark.parametrize("config", TR_CONFIGS[1:])
@@ -418,6 +451,7 @@ def run_hip_scaled(q, pool, table, start, layer, scale, out=None):
 SCALE_CASES = [
     # dtype, start, T, H, D, kernel configuration, keys per partition (0: whole)
     (torch.bfloat16, 100, 130, 4, 128, "1422", "0"),
+    (torch.bfloat16, 100, 130, 4, 128, "11422", "0"),
     (torch.bfloat16, 100, 130, 4, 128, "412", "0"),
     (torch.bfloat16, 100, 130, 4, 128, "0", "0"),
     (torch.float16, 100, 130, 4, 128, "-1", "0"),
@@ -429,7 +463,7 @@ SCALE_CASES = [
 @pytest.mark.parametrize("scale", [-1 / math.sqrt(128), -0.3, 0.0, 0.3, 4.0],
                          ids=["neg_rsqrt", "neg", "zero", "pos", "large"])
 @pytest.mark.parametrize("dtype,start,T,H,D,config,split", SCALE_CASES,
-                         ids=["bf16_1422", "bf16_412", "bf16_mfma", "f16", "f32", "bf16_split"])
+                         ids=["bf16_1422", "bf16_paired", "bf16_412", "bf16_mfma", "f16", "f32", "bf16_split"])
 def test_any_finite_scale_matches_oracle(monkeypatch, dtype, start, T, H, D, config, split, scale):
     """softmax(scale * q.k) for negative, zero and positive scales: the kernels
     take maxima over raw scores, so a negative scale is carried by the query's
