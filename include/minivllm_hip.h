@@ -60,7 +60,8 @@ const char* mgi_last_error(void);
 /* ABI version of this library (major*100 + minor). 1.01 added
  * mgi_paged_decode_balanced_waves and the even split of split_tokens = 0;
  * 1.02 the prefill key split (mgi_paged_prefill's workspace arguments and
- * mgi_paged_prefill_workspace_bytes); 1.03 mgi_paged_decode_noalloc. */
+ * mgi_paged_prefill_workspace_bytes); 1.03 mgi_paged_decode_noalloc; 1.04
+ * mgi_paged_decode_append. */
 int mgi_abi_version(void);
 
 /*
@@ -143,6 +144,48 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, /* [3] */
                      float scale, int64_t split_tokens,
                      void* workspace, size_t workspace_bytes,
                      void* stream);
+
+/*
+ * One decode step's KV append and attention in one call: mgi_kv_append of the
+ * B rows k_new[b], v_new[b] ([B, H, D]) into slots slot_mapping[b] ([B]),
+ * then mgi_paged_decode, on the same stream. Replaces the slot write and the
+ * backend call of KVCacheCausalSelfAttention.forward_decode_batch
+ * (minivllm/attention.py:370-416), which the reference issues one after the
+ * other.
+ *
+ * Contract beyond the two calls': a slot that some sequence's context reads
+ * must be the slot of its own row's last context position (block_tables[b,
+ * (c-1)/S]*S + (c-1)%S, c = context_lens[b] clamped as in mgi_paged_decode),
+ * as in decode, where row b holds sequence b's newest token. Negative slots,
+ * slots outside the pool and slots no context reads are free. Under it the
+ * pool and out are bit-identical to those of the two calls.
+ *
+ * On the fast path, with new_dtype == dtype, a unit head-dim stride and
+ * 16-byte aligned rows, the append runs inside the attention launch: the
+ * wavefront that streams a sequence's last block writes that row's slot
+ * first (one launch fewer per step). Otherwise the append kernel runs first
+ * (conversions as mgi_kv_append). Workspace as mgi_paged_decode for the same
+ * sizes. Added in ABI 1.04.
+ */
+int mgi_paged_decode_append(void* out, const int64_t* out_strides, /* [3] */
+                            const void* q, const int64_t* q_strides, /* [3] */
+                            void* k_pool, void* v_pool,
+                            const int64_t* k_pool_strides, /* [5] */
+                            const int64_t* v_pool_strides, /* [5] */
+                            int dtype,
+                            const void* k_new, const void* v_new,
+                            const int64_t* k_new_strides, /* [3] */
+                            const int64_t* v_new_strides, /* [3] */
+                            int new_dtype,
+                            const void* slot_mapping, int64_t slot_stride, int slot_itype,
+                            const void* block_tables, const int64_t* bt_strides, /* [2] */
+                            int bt_itype,
+                            const void* context_lens, int64_t cl_stride, int cl_itype,
+                            int64_t B, int64_t H, int64_t D, int64_t S, int64_t N,
+                            int64_t M, int64_t L, int64_t layer_idx,
+                            float scale, int64_t split_tokens,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /*
  * mgi_paged_decode without a workspace argument, for callers that cannot

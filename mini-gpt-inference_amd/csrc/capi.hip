@@ -320,7 +320,7 @@ extern "C" {
 
 const char* mgi_last_error(void) { return g_err.c_str(); }
 
-int mgi_abi_version(void) { return 103; }
+int mgi_abi_version(void) { return 104; }
 
 int64_t mgi_paged_decode_split_tokens(int64_t B, int64_t H, int64_t D, int64_t S, int64_t M,
                                       int64_t split_tokens) {
@@ -349,10 +349,98 @@ size_t mgi_paged_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t
 
 namespace {
 
-// The body of mgi_paged_decode and mgi_paged_decode_noalloc. When
-// `scratch_dev` >= 0 the workspace is that device's allocation-free scratch
-// (resolved here once the call is known to need it, after every check has
-// passed); otherwise it is the caller's `workspace`.
+// The new rows of a KV append: mgi_kv_append's arguments, and those of
+// mgi_paged_decode_append's append.
+struct AppendSpec {
+  void* k_pool;
+  void* v_pool;
+  const void* k_new;
+  const void* v_new;
+  const int64_t* kn_strides;  // [3]
+  const int64_t* vn_strides;  // [3]
+  int new_dtype;
+  const void* slots;
+  int64_t slot_stride;
+  int slot_itype;
+};
+
+// Checks of the new rows (the pool's are the caller's).
+int check_append(const AppendSpec& ap, int pool_dtype, int64_t T) {
+  if (!ap.k_new || !ap.v_new || !ap.slots) return fail(MGI_EINVAL, "null tensor pointer");
+  if (!ap.kn_strides || !ap.vn_strides) return fail(MGI_EINVAL, "null stride array");
+  if (!valid_dtype(ap.new_dtype)) return fail(MGI_EINVAL, "unknown dtype code");
+  if (!valid_itype(ap.slot_itype)) return fail(MGI_EINVAL, "slot_mapping must be int32 or int64");
+  if (!nonneg(ap.kn_strides, 3) || !nonneg(ap.vn_strides, 3) || ap.slot_stride < 0)
+    return fail(MGI_EINVAL, "strides must be non-negative");
+  if (T > (int64_t(1) << 31) - 1) return fail(MGI_EUNSUPPORTED, "too many rows");
+  if (pool_dtype != ap.new_dtype && pool_dtype != MGI_F32 && ap.new_dtype != MGI_F32)
+    return fail(MGI_EUNSUPPORTED, "only same-dtype copies and conversions to/from f32");
+  return MGI_OK;
+}
+
+// Launches the append kernel for T checked rows.
+int launch_append(const AppendSpec& ap, const int64_t* k_pool_strides, const int64_t* v_pool_strides,
+                  int pool_dtype, int64_t T, int64_t H, int64_t D, int64_t S, int64_t N,
+                  int64_t layer_idx, hipStream_t stream) {
+  using namespace mgi;
+  const int new_dtype = ap.new_dtype;
+  const int64_t* k_new_strides = ap.kn_strides;
+  const int64_t* v_new_strides = ap.vn_strides;
+  const int64_t peb = dtype_bytes(pool_dtype), neb = dtype_bytes(new_dtype);
+  char* kbase = static_cast<char*>(ap.k_pool) + layer_idx * k_pool_strides[0] * peb;
+  char* vbase = static_cast<char*>(ap.v_pool) + layer_idx * v_pool_strides[0] * peb;
+
+  AppendArgs a{};
+  a.kp = kbase;
+  a.vp = vbase;
+  a.k_sn = k_pool_strides[1];
+  a.k_ss = k_pool_strides[2];
+  a.k_sh = k_pool_strides[3];
+  a.k_sd = k_pool_strides[4];
+  a.v_sn = v_pool_strides[1];
+  a.v_ss = v_pool_strides[2];
+  a.v_sh = v_pool_strides[3];
+  a.v_sd = v_pool_strides[4];
+  a.kn = ap.k_new;
+  a.vn = ap.v_new;
+  a.kn_st = k_new_strides[0];
+  a.kn_sh = k_new_strides[1];
+  a.kn_sd = k_new_strides[2];
+  a.vn_st = v_new_strides[0];
+  a.vn_sh = v_new_strides[1];
+  a.vn_sd = v_new_strides[2];
+  a.slots = ap.slots;
+  a.sl_s = ap.slot_stride;
+  a.sl_i64 = ap.slot_itype == MGI_I64;
+  a.T = (int)T;
+  a.H = (int)H;
+  a.D = (int)D;
+  a.S = (int)S;
+  a.N = N;
+
+  const bool rows_contig = k_pool_strides[4] == 1 && k_pool_strides[3] == D &&
+                           v_pool_strides[4] == 1 && v_pool_strides[3] == D &&
+                           k_new_strides[2] == 1 && k_new_strides[1] == D &&
+                           v_new_strides[2] == 1 && v_new_strides[1] == D;
+  const bool vector_path = pool_dtype == new_dtype && rows_contig && mult16(H * D, peb) &&
+                           aligned16(kbase) && aligned16(vbase) && aligned16(ap.k_new) &&
+                           aligned16(ap.v_new) && mult16(k_pool_strides[1], peb) &&
+                           mult16(k_pool_strides[2], peb) && mult16(v_pool_strides[1], peb) &&
+                           mult16(v_pool_strides[2], peb) && mult16(k_new_strides[0], neb) &&
+                           mult16(v_new_strides[0], neb);
+
+  const hipError_t e = launch_kv_append(a, pool_dtype, new_dtype, vector_path, stream);
+  if (e != hipSuccess) return fail(MGI_ELAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
+  return MGI_OK;
+}
+
+// The body of mgi_paged_decode, mgi_paged_decode_noalloc and
+// mgi_paged_decode_append. With `use_scratch` the workspace is the device's
+// allocation-free scratch (resolved here once the call is known to need it,
+// after every check has passed); otherwise it is the caller's `workspace`.
+// With `ap`, B new rows are appended first: inside the decode launch on the
+// fast path when the rows share the pool's dtype and are 16-byte aligned with
+// a contiguous head dim, else by the append kernel launched before it.
 int paged_decode_impl(void* out, const int64_t* out_strides, const void* q,
                       const int64_t* q_strides, const void* k_pool, const void* v_pool,
                       const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
@@ -360,7 +448,7 @@ int paged_decode_impl(void* out, const int64_t* out_strides, const void* q,
                       const void* context_lens, int64_t cl_stride, int cl_itype, int64_t B,
                       int64_t H, int64_t D, int64_t S, int64_t N, int64_t M, int64_t L,
                       int64_t layer_idx, float scale, int64_t split_tokens, void* workspace,
-                      size_t workspace_bytes, bool use_scratch, void* stream) {
+                      size_t workspace_bytes, bool use_scratch, const AppendSpec* ap, void* stream) {
   using namespace mgi;
   g_err.clear();
   if (!out || !q || !k_pool || !v_pool || !block_tables || !context_lens)
@@ -383,6 +471,10 @@ int paged_decode_impl(void* out, const int64_t* out_strides, const void* q,
     return fail(MGI_EUNSUPPORTED, "block table wider than 65535 partitions");
   if (M * S >= (int64_t(1) << 31)) return fail(MGI_EUNSUPPORTED, "M*S must be < 2^31");
   if (D > 512) return fail(MGI_EUNSUPPORTED, "head_dim larger than 512");
+  if (ap) {
+    const int rc = check_append(*ap, dtype, B);
+    if (rc != MGI_OK) return rc;
+  }
 
   const int64_t eb = dtype_bytes(dtype);
   const char* kbase = static_cast<const char*>(k_pool) + layer_idx * k_pool_strides[0] * eb;
@@ -491,6 +583,31 @@ int paged_decode_impl(void* out, const int64_t* out_strides, const void* q,
     }
   }
 
+  if (ap) {
+    const int64_t* ks = ap->kn_strides;
+    const int64_t* vs = ap->vn_strides;
+    const bool fuse = plan.path == DecodePath::kFast && ap->new_dtype == dtype && ks[2] == 1 &&
+                      vs[2] == 1 && aligned16(ap->k_new) && aligned16(ap->v_new) &&
+                      mult16(ks[0], eb) && mult16(ks[1], eb) && mult16(vs[0], eb) && mult16(vs[1], eb);
+    if (fuse) {
+      a.kw = static_cast<char*>(ap->k_pool) + layer_idx * k_pool_strides[0] * eb;
+      a.vw = static_cast<char*>(ap->v_pool) + layer_idx * v_pool_strides[0] * eb;
+      a.kn = ap->k_new;
+      a.vn = ap->v_new;
+      a.kn_sb = ks[0];
+      a.kn_sh = ks[1];
+      a.vn_sb = vs[0];
+      a.vn_sh = vs[1];
+      a.slots = ap->slots;
+      a.sl_s = ap->slot_stride;
+      a.sl_i64 = ap->slot_itype == MGI_I64;
+    } else {
+      const int rc = launch_append(*ap, k_pool_strides, v_pool_strides, dtype, B, H, D, S, N, layer_idx,
+                                   static_cast<hipStream_t>(stream));
+      if (rc != MGI_OK) return rc;
+    }
+  }
+
   // The merge runs one workgroup per (sequence, head group). When those are
   // few, each folds many partials in a chain of dependent loads; give it up
   // to 8 wavefronts, so the merge has about two per CU. Measured on MI355X
@@ -521,7 +638,26 @@ int mgi_paged_decode(void* out, const int64_t* out_strides, const void* q,
   return paged_decode_impl(out, out_strides, q, q_strides, k_pool, v_pool, k_pool_strides,
                            v_pool_strides, dtype, block_tables, bt_strides, bt_itype, context_lens,
                            cl_stride, cl_itype, B, H, D, S, N, M, L, layer_idx, scale, split_tokens,
-                           workspace, workspace_bytes, false, stream);
+                           workspace, workspace_bytes, false, nullptr, stream);
+}
+
+int mgi_paged_decode_append(void* out, const int64_t* out_strides, const void* q,
+                            const int64_t* q_strides, void* k_pool, void* v_pool,
+                            const int64_t* k_pool_strides, const int64_t* v_pool_strides, int dtype,
+                            const void* k_new, const void* v_new, const int64_t* k_new_strides,
+                            const int64_t* v_new_strides, int new_dtype, const void* slot_mapping,
+                            int64_t slot_stride, int slot_itype, const void* block_tables,
+                            const int64_t* bt_strides, int bt_itype, const void* context_lens,
+                            int64_t cl_stride, int cl_itype, int64_t B, int64_t H, int64_t D,
+                            int64_t S, int64_t N, int64_t M, int64_t L, int64_t layer_idx,
+                            float scale, int64_t split_tokens, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  const AppendSpec ap{k_pool, v_pool, k_new, v_new, k_new_strides, v_new_strides, new_dtype,
+                      slot_mapping, slot_stride, slot_itype};
+  return paged_decode_impl(out, out_strides, q, q_strides, k_pool, v_pool, k_pool_strides,
+                           v_pool_strides, dtype, block_tables, bt_strides, bt_itype, context_lens,
+                           cl_stride, cl_itype, B, H, D, S, N, M, L, layer_idx, scale, split_tokens,
+                           workspace, workspace_bytes, false, &ap, stream);
 }
 
 int mgi_paged_decode_noalloc(void* out, const int64_t* out_strides, const void* q,
@@ -535,7 +671,7 @@ int mgi_paged_decode_noalloc(void* out, const int64_t* out_strides, const void* 
   return paged_decode_impl(out, out_strides, q, q_strides, k_pool, v_pool, k_pool_strides,
                            v_pool_strides, dtype, block_tables, bt_strides, bt_itype, context_lens,
                            cl_stride, cl_itype, B, H, D, S, N, M, L, layer_idx, scale, split_tokens,
-                           nullptr, 0, true, stream);
+                           nullptr, 0, true, nullptr, stream);
 }
 
 int mgi_kv_append(void* k_pool, void* v_pool, const int64_t* k_pool_strides,
@@ -548,69 +684,19 @@ int mgi_kv_append(void* k_pool, void* v_pool, const int64_t* k_pool_strides,
   g_err.clear();
   if (T < 0) return fail(MGI_EINVAL, "row count must be non-negative");
   if (T == 0) return MGI_OK;
-  if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping)
-    return fail(MGI_EINVAL, "null tensor pointer");
-  if (!k_pool_strides || !v_pool_strides || !k_new_strides || !v_new_strides)
-    return fail(MGI_EINVAL, "null stride array");
+  if (!k_pool || !v_pool) return fail(MGI_EINVAL, "null tensor pointer");
+  if (!k_pool_strides || !v_pool_strides) return fail(MGI_EINVAL, "null stride array");
   if (H <= 0 || D <= 0 || S <= 0 || N <= 0 || L <= 0)
     return fail(MGI_EINVAL, "pool dimensions must be nonzero");
   if (layer_idx < 0 || layer_idx >= L) return fail(MGI_EINVAL, "layer_idx outside KV pool");
-  if (!valid_dtype(pool_dtype) || !valid_dtype(new_dtype)) return fail(MGI_EINVAL, "unknown dtype code");
-  if (!valid_itype(slot_itype)) return fail(MGI_EINVAL, "slot_mapping must be int32 or int64");
-  if (!nonneg(k_pool_strides, 5) || !nonneg(v_pool_strides, 5) || !nonneg(k_new_strides, 3) ||
-      !nonneg(v_new_strides, 3) || slot_stride < 0)
-    return fail(MGI_EINVAL, "strides must be non-negative");
-  if (T > (int64_t(1) << 31) - 1) return fail(MGI_EUNSUPPORTED, "too many rows");
-  if (pool_dtype != new_dtype && pool_dtype != MGI_F32 && new_dtype != MGI_F32)
-    return fail(MGI_EUNSUPPORTED, "only same-dtype copies and conversions to/from f32");
-
-  const int64_t peb = dtype_bytes(pool_dtype), neb = dtype_bytes(new_dtype);
-  char* kbase = static_cast<char*>(k_pool) + layer_idx * k_pool_strides[0] * peb;
-  char* vbase = static_cast<char*>(v_pool) + layer_idx * v_pool_strides[0] * peb;
-
-  AppendArgs a{};
-  a.kp = kbase;
-  a.vp = vbase;
-  a.k_sn = k_pool_strides[1];
-  a.k_ss = k_pool_strides[2];
-  a.k_sh = k_pool_strides[3];
-  a.k_sd = k_pool_strides[4];
-  a.v_sn = v_pool_strides[1];
-  a.v_ss = v_pool_strides[2];
-  a.v_sh = v_pool_strides[3];
-  a.v_sd = v_pool_strides[4];
-  a.kn = k_new;
-  a.vn = v_new;
-  a.kn_st = k_new_strides[0];
-  a.kn_sh = k_new_strides[1];
-  a.kn_sd = k_new_strides[2];
-  a.vn_st = v_new_strides[0];
-  a.vn_sh = v_new_strides[1];
-  a.vn_sd = v_new_strides[2];
-  a.slots = slot_mapping;
-  a.sl_s = slot_stride;
-  a.sl_i64 = slot_itype == MGI_I64;
-  a.T = (int)T;
-  a.H = (int)H;
-  a.D = (int)D;
-  a.S = (int)S;
-  a.N = N;
-
-  const bool rows_contig = k_pool_strides[4] == 1 && k_pool_strides[3] == D &&
-                           v_pool_strides[4] == 1 && v_pool_strides[3] == D &&
-                           k_new_strides[2] == 1 && k_new_strides[1] == D &&
-                           v_new_strides[2] == 1 && v_new_strides[1] == D;
-  const bool vector_path = pool_dtype == new_dtype && rows_contig && mult16(H * D, peb) &&
-                           aligned16(kbase) && aligned16(vbase) && aligned16(k_new) &&
-                           aligned16(v_new) && mult16(k_pool_strides[1], peb) &&
-                           mult16(k_pool_strides[2], peb) && mult16(v_pool_strides[1], peb) &&
-                           mult16(v_pool_strides[2], peb) && mult16(k_new_strides[0], neb) &&
-                           mult16(v_new_strides[0], neb);
-
-  const hipError_t e =
-      launch_kv_append(a, pool_dtype, new_dtype, vector_path, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return fail(MGI_ELAUNCH, std::string("launch failed: ") + hipGetErrorString(e));
-  return MGI_OK;
+  if (!valid_dtype(pool_dtype)) return fail(MGI_EINVAL, "unknown dtype code");
+  if (!nonneg(k_pool_strides, 5) || !nonneg(v_pool_strides, 5)) return fail(MGI_EINVAL, "strides must be non-negative");
+  const AppendSpec ap{k_pool, v_pool, k_new, v_new, k_new_strides, v_new_strides, new_dtype,
+                      slot_mapping, slot_stride, slot_itype};
+  const int rc = check_append(ap, pool_dtype, T);
+  if (rc != MGI_OK) return rc;
+  return launch_append(ap, k_pool_strides, v_pool_strides, pool_dtype, T, H, D, S, N, layer_idx,
+                       static_cast<hipStream_t>(stream));
 }
 
 int mgi_paged_prefill(void* out, const int64_t* out_strides, const void* q,

@@ -40,6 +40,19 @@ struct DecodeArgs {
   float2* ws_ml;      // [B, H, max_parts]    partial (max, sum), log2 domain
   int* ws_cinc;       // balanced mode: [B] inclusive prefix sums of blocks per sequence
   int* ws_ticket;     // balanced mode: one ticket counter per head group
+  // Fused KV append (fast path only; kw == nullptr: none). Row b of kn / vn
+  // ([B, H, D], head dim contiguous, rows 16-byte aligned) goes to pool slot
+  // slots[b] (skipped when outside [0, N*S)), written by each head group's
+  // wavefront that streams sequence b's last block, before it reads that
+  // block; rows of sequences with no blocks by a wavefront of their own.
+  void* kw;           // the pool at layer layer_idx (k, v), writable
+  void* vw;
+  const void* kn;
+  const void* vn;
+  int64_t kn_sb, kn_sh, vn_sb, vn_sh;
+  const void* slots;
+  int64_t sl_s;
+  int sl_i64;
 };
 
 // KV append / scatter. Pool pointers already point at layer layer_idx.

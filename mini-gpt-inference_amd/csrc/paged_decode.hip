@@ -28,6 +28,13 @@
 // partials that paged_decode_merge combines:
 //   M = max_p m_p,  L = sum_p l_p 2^(m_p - M),  O = sum_p O_p 2^(m_p - M) / L.
 //
+// Fused KV append (mgi_paged_decode_append, fast path): the wavefront of a
+// head group that streams sequence b's last block first copies that head
+// group's slice of row b of the new K/V to pool slot slot_mapping[b], then
+// streams the block; it reads the slot after writing it, in program order,
+// so attention sees exactly the pool a separate append would have left. A
+// row whose sequence has no blocks is copied by a wavefront of its own.
+//
 // The fast path covers bf16, f16 (the same lane layout, v_dot2_f32_f16) and
 // f32. Generic path (paged_decode_generic): any strides, head_dim up to 512,
 // any block size, f32/bf16/f16; one wavefront per (b, h), one token at a time.
@@ -184,12 +191,60 @@ __device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h, in
            a.D);
 }
 
+// Fused append, in two halves so their latencies overlap the caller's
+// loads: append_load issues this lane's loads of piece j (0, and 1 for f32)
+// of head h of row b of the new K and V; append_store writes a piece to pool
+// slot `slot`. append_fence keeps every later load of this wavefront behind
+// the stores in the compiler's order; the hardware keeps a wavefront's
+// accesses to one address in order.
+template <typename T>
+__device__ __forceinline__ void append_load(const DecodeArgs& a, int b, int h, int sub, int j, uint4& kf,
+                                            uint4& vf) {
+  constexpr int EB = (int)sizeof(T);
+  const int o = Layout<T>::load_off(sub, a.D, j) * EB;
+  kf = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(a.kn) +
+                                       ((int64_t)b * a.kn_sb + (int64_t)h * a.kn_sh) * EB + o);
+  vf = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(a.vn) +
+                                       ((int64_t)b * a.vn_sb + (int64_t)h * a.vn_sh) * EB + o);
+}
+template <typename T>
+__device__ __forceinline__ void append_store(const DecodeArgs& a, int64_t slot, int h, int sub, int j,
+                                             const uint4& kf, const uint4& vf) {
+  constexpr int EB = (int)sizeof(T);
+  const int64_t blk = slot / a.S, off = slot - blk * (int64_t)a.S;
+  const int o = Layout<T>::load_off(sub, a.D, j) * EB;
+  *reinterpret_cast<uint4*>(reinterpret_cast<char*>(a.kw) +
+                            (blk * a.k_sn + off * a.k_ss + (int64_t)h * a.k_sh) * EB + o) = kf;
+  *reinterpret_cast<uint4*>(reinterpret_cast<char*>(a.vw) +
+                            (blk * a.v_sn + off * a.v_ss + (int64_t)h * a.v_sh) * EB + o) = vf;
+}
+__device__ __forceinline__ bool append_slot_ok(const DecodeArgs& a, int64_t slot) {
+  return slot >= 0 && slot < a.N * (int64_t)a.S;
+}
+__device__ __forceinline__ void append_fence() { __atomic_signal_fence(__ATOMIC_SEQ_CST); }
+
+// The fused append of one row in one go (rows of sequences with no blocks).
+template <typename T, bool FULL>
+__device__ __forceinline__ void append_row(const DecodeArgs& a, int b, int h, int sub, bool lane_ok) {
+  const int64_t slot = load_index(a.slots, a.sl_i64, (int64_t)b * a.sl_s);
+  if (!append_slot_ok(a, slot)) return;  // uniform
+  if (FULL || lane_ok) {
+#pragma unroll
+    for (int j = 0; j < Layout<T>::kLoads; ++j) {
+      uint4 kf, vf;
+      append_load<T>(a, b, h, sub, j, kf, vf);
+      append_store<T>(a, slot, h, sub, j, kf, vf);
+    }
+  }
+  append_fence();
+}
+
 // Folds the tokens of blocks [blk_begin, blk_end) of sequence b, clipped to
 // its context ctx, into the wave's online-softmax state (m, l, acc); the
 // chunk spans at most kMaxBlocksPerPart blocks. Scores live in the log2
 // domain.
 template <typename T, int LPH, int TOK, bool FULL>
-__device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane, bool lane_ok,
+__device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int h, int lane, bool lane_ok,
                                             const QFrag<T>& q,
                                             const uint32_t (&koff)[Layout<T>::kLoads],
                                             const uint32_t (&voff)[Layout<T>::kLoads],
@@ -223,6 +278,32 @@ __device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane,
       const int64_t e = load_index(a.bt, a.bt_i64, bt_row + (int64_t)(c0 + 64 + lane) * a.bt_sm);
       phys_hi = (e >= 0 && e < a.N) ? (int)e : -1;
     }
+    // The chunk holding the sequence's last token writes the fused append's
+    // row: its loads go out beside the table entries', its stores just before
+    // the loads of the chunk's last step, which reads the new token. Stores
+    // count in the same in-order wait counter as loads, so stores issued
+    // earlier would hold up the waits of the steps in between: at B=256,
+    // 32 heads, stores before step 1 cost 8.7 us over decode alone, stores
+    // before the last step 5.7 (the append kernel and its launch 6.3); at
+    // B=64, 3.8 against 1.6 (4.4).
+    const bool tail = a.kw != nullptr && t_end == ctx;
+    const int asub = lane % LPH;
+    const bool aok = FULL || lane_ok;
+    uint4 ak0, av0, ak1, av1;
+    int64_t aslot = -1;
+    if (tail) {
+      if (aok) append_load<T>(a, b, h, asub, 0, ak0, av0);
+      if (aok && NL == 2) append_load<T>(a, b, h, asub, 1, ak1, av1);
+      aslot = load_index(a.slots, a.sl_i64, (int64_t)b * a.sl_s);
+    }
+    auto append_stores = [&]() {
+      if (!tail) return;
+      if (append_slot_ok(a, aslot) && aok) {
+        append_store<T>(a, aslot, h, asub, 0, ak0, av0);
+        if (NL == 2) append_store<T>(a, aslot, h, asub, 1, ak1, av1);
+      }
+      append_fence();
+    };
 
     // Issues the K/V loads of step s and returns its number of valid tokens
     // (0 past the chunk or for a masked block). Every iteration issues the
@@ -231,6 +312,7 @@ __device__ __forceinline__ void fold_chunk(const DecodeArgs& a, int b, int lane,
     // per wave: the streaming loads are non-temporal, so re-reading the whole
     // last step would fetch it from HBM again).
     auto issue = [&](int s, Step<T, TOK>& st) -> int {
+      if (s == nsteps - 1) append_stores();
       const bool past = s >= nsteps;
       const int sc = past ? nsteps - 1 : s;
       const int rel = sc / steps_per_blk;
@@ -354,7 +436,8 @@ paged_decode_fast(const DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   const int bpp = P / a.S;  // P is a multiple of S
-  fold_chunk<T, LPH, TOK, FULL>(a, b, lane, lane_ok, q, koff, voff, part * bpp, (part + 1) * bpp, ctx,
+  if (a.kw != nullptr && ctx == 0 && part == 0) append_row<T, FULL>(a, b, h, sub, lane_ok);
+  fold_chunk<T, LPH, TOK, FULL>(a, b, h, lane, lane_ok, q, koff, voff, part * bpp, (part + 1) * bpp, ctx,
                                  m, l, acc);
   finish_piece<T>(a, b, h, sub, lane_ok, m, l, acc, nparts, ((size_t)b * a.H + h) * a.max_parts + part);
 }
@@ -518,6 +601,26 @@ paged_decode_fast_bal(const DecodeArgs a) {
   uint32_t koff[Layout<T>::kLoads], voff[Layout<T>::kLoads];
   row_offsets<T>(a, h, sub, lane_ok, koff, voff);
 
+  // Fused append of rows whose sequence has no blocks (no wavefront streams
+  // them; padding rows, slot -1, are among them): wave w of each head group
+  // checks rows 64 w .. 64 w + 63, one per lane.
+  if (a.kw != nullptr) {
+    for (int b0 = 64 * w; b0 < a.B; b0 += 64 * a.bal_waves) {
+      const int bb = b0 + lane;
+      bool write = false;
+      if (bb < a.B && cinc[bb] == (bb > 0 ? cinc[bb - 1] : 0)) {
+        const int64_t slot = load_index(a.slots, a.sl_i64, (int64_t)bb * a.sl_s);
+        write = slot >= 0 && slot < a.N * (int64_t)a.S;
+      }
+      uint64_t rows = __builtin_amdgcn_ballot_w64(write);
+      while (rows) {
+        const int i = __builtin_ctzll(rows);
+        rows &= rows - 1;
+        append_row<T, FULL>(a, b0 + i, h, sub, lane_ok);
+      }
+    }
+  }
+
   // Streams claim c: one flat loop over chunks of at most kMaxBlocksPerPart
   // blocks of one sequence; the state is written out when the wave leaves a
   // sequence.
@@ -551,7 +654,7 @@ paged_decode_fast_bal(const DecodeArgs a) {
         for (int i = 0; i < 8; ++i) acc[i] = 0.f;
       }
       const int ch_end = min(min(end, ce), pos + kMaxBlocksPerPart);
-      fold_chunk<T, LPH, TOK, FULL>(a, b, lane, lane_ok, q, koff, voff, pos - cb, ch_end - cb, ctx, m, l,
+      fold_chunk<T, LPH, TOK, FULL>(a, b, h, lane, lane_ok, q, koff, voff, pos - cb, ch_end - cb, ctx, m, l,
                                     acc);
       pos = ch_end;
       if (pos == ce || pos == end) {

@@ -82,10 +82,10 @@ void kv_append(const at::Tensor& kp, const at::Tensor& vp, int64_t layer_idx, co
                              slots.data_ptr(), slots.stride(0), st, T, H, D, S, N, L, layer_idx, stream_of(kp)));
 }
 
-// paged_decode(q, k_pool, v_pool, block_tables, context_lengths, layer_idx,
-// split_tokens) -> [B, H, D] attention output of q's dtype.
-at::Tensor paged_decode(const at::Tensor& q, const at::Tensor& kp, const at::Tensor& vp, const at::Tensor& bt,
-                        const at::Tensor& cl, int64_t layer_idx, int64_t split_tokens) {
+// Checks of paged_decode's arguments (the Triton v0 backend's order and
+// messages); returns the block-table width M.
+int64_t check_decode(const at::Tensor& q, const at::Tensor& kp, const at::Tensor& vp, const at::Tensor& bt,
+                     const at::Tensor& cl, int64_t layer_idx) {
   if (!q.is_cuda()) value_error("q must be on a GPU device for the HIP backend");
   if (q.dim() != 3) value_error("q must have shape [B,H,D]");
   const int64_t b = q.size(0), h = q.size(1), d = q.size(2);
@@ -96,30 +96,73 @@ at::Tensor paged_decode(const at::Tensor& q, const at::Tensor& kp, const at::Ten
   if (kp.scalar_type() != q.scalar_type() || vp.scalar_type() != q.scalar_type())
     value_error("KV pool dtype must match q dtype");
   check_pool(kp, vp);
-  const int64_t L = kp.size(0), N = kp.size(1), S = kp.size(2);
+  const int64_t L = kp.size(0), S = kp.size(2);
   if (S <= 0) value_error("block_size must be positive");
   if (kp.size(3) != h || kp.size(4) != d) value_error("KV head dimensions or block size do not match q");
   if (bt.dim() != 2 || bt.size(0) != b) value_error("block_tables must have shape [B,M]");
   if (cl.dim() != 1 || cl.size(0) != b) value_error("context_lengths must have shape [B]");
-  const int bti = index_code(bt.scalar_type());
-  if (bti < 0) value_error("block_tables must contain integer indices");
-  const int cli = index_code(cl.scalar_type());
-  if (cli < 0) value_error("context_lengths must be integer");
+  if (index_code(bt.scalar_type()) < 0) value_error("block_tables must contain integer indices");
+  if (index_code(cl.scalar_type()) < 0) value_error("context_lengths must be integer");
   if (layer_idx < 0 || layer_idx >= L) value_error("layer_idx outside KV pool");
   const auto dev = q.device();
   if (kp.device() != dev || vp.device() != dev || bt.device() != dev || cl.device() != dev)
     value_error("all inputs must reside on same GPU device");
   const int64_t M = bt.size(1);
   if (M < 1) value_error("block_tables need at least one block column");
+  return M;
+}
+
+// paged_decode(q, k_pool, v_pool, block_tables, context_lengths, layer_idx,
+// split_tokens) -> [B, H, D] attention output of q's dtype.
+at::Tensor paged_decode(const at::Tensor& q, const at::Tensor& kp, const at::Tensor& vp, const at::Tensor& bt,
+                        const at::Tensor& cl, int64_t layer_idx, int64_t split_tokens) {
+  const int64_t M = check_decode(q, kp, vp, bt, cl, layer_idx);
+  const int64_t b = q.size(0), h = q.size(1), d = q.size(2), L = kp.size(0), N = kp.size(1), S = kp.size(2);
   at::Tensor out = at::empty({b, h, d}, q.options());
   const size_t ws_bytes = mgi_paged_decode_workspace_bytes(b, h, d, S, M, split_tokens);
   at::Tensor ws;
   if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, q.options().dtype(at::kByte));
   check_status(mgi_paged_decode(out.data_ptr(), out.strides().data(), q.data_ptr(), q.strides().data(),
-                                kp.data_ptr(), vp.data_ptr(), kp.strides().data(), vp.strides().data(), qd,
-                                bt.data_ptr(), bt.strides().data(), bti, cl.data_ptr(), cl.stride(0), cli, b, h, d,
-                                S, N, M, L, layer_idx, (float)(1.0 / std::sqrt((double)d)), split_tokens,
+                                kp.data_ptr(), vp.data_ptr(), kp.strides().data(), vp.strides().data(),
+                                dtype_code(q.scalar_type()), bt.data_ptr(), bt.strides().data(),
+                                index_code(bt.scalar_type()), cl.data_ptr(), cl.stride(0),
+                                index_code(cl.scalar_type()), b, h, d, S, N, M, L, layer_idx,
+                                (float)(1.0 / std::sqrt((double)d)), split_tokens,
                                 ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q)));
+  return out;
+}
+
+// paged_decode_append(q, k_pool, v_pool, block_tables, context_lengths,
+// layer_idx, k, v, slot_mapping, split_tokens) -> [B, H, D]: kv_append of
+// the B rows k[b], v[b] into slot_mapping[b], then paged_decode, as one call
+// (one launch fewer where the library fuses them).
+at::Tensor paged_decode_append(const at::Tensor& q, const at::Tensor& kp, const at::Tensor& vp,
+                               const at::Tensor& bt, const at::Tensor& cl, int64_t layer_idx, const at::Tensor& k,
+                               const at::Tensor& v, const at::Tensor& slots, int64_t split_tokens) {
+  const int64_t M = check_decode(q, kp, vp, bt, cl, layer_idx);
+  const int64_t b = q.size(0), h = q.size(1), d = q.size(2), L = kp.size(0), N = kp.size(1), S = kp.size(2);
+  if (k.dim() != 3 || v.sizes() != k.sizes()) value_error("k and v must have matching shape [T,H,D]");
+  if (k.size(0) != b) value_error("k and v must hold one row per sequence");
+  if (k.size(1) != h || k.size(2) != d) value_error("k/v head dimensions do not match the KV pool");
+  const int nd = dtype_code(k.scalar_type());
+  if (nd < 0 || v.scalar_type() != k.scalar_type()) value_error("k and v must share a float dtype");
+  if (slots.dim() != 1 || slots.size(0) != b) value_error("slot_mapping must have shape [B]");
+  const int st = index_code(slots.scalar_type());
+  if (st < 0) value_error("slot_mapping must contain integer slots");
+  const auto dev = q.device();
+  if (k.device() != dev || v.device() != dev || slots.device() != dev)
+    value_error("all inputs must reside on same GPU device");
+  at::Tensor out = at::empty({b, h, d}, q.options());
+  const size_t ws_bytes = mgi_paged_decode_workspace_bytes(b, h, d, S, M, split_tokens);
+  at::Tensor ws;
+  if (ws_bytes) ws = at::empty({(int64_t)ws_bytes}, q.options().dtype(at::kByte));
+  check_status(mgi_paged_decode_append(
+      out.data_ptr(), out.strides().data(), q.data_ptr(), q.strides().data(), kp.data_ptr(), vp.data_ptr(),
+      kp.strides().data(), vp.strides().data(), dtype_code(q.scalar_type()), k.data_ptr(), v.data_ptr(),
+      k.strides().data(), v.strides().data(), nd, slots.data_ptr(), slots.stride(0), st, bt.data_ptr(),
+      bt.strides().data(), index_code(bt.scalar_type()), cl.data_ptr(), cl.stride(0), index_code(cl.scalar_type()),
+      b, h, d, S, N, M, L, layer_idx, (float)(1.0 / std::sqrt((double)d)), split_tokens,
+      ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q)));
   return out;
 }
 
@@ -164,8 +207,9 @@ at::Tensor paged_prefill(const at::Tensor& q, const at::Tensor& kp, const at::Te
 }  // namespace
 
 PYBIND11_MODULE(_hip_ops, m) {
-  m.doc() = "PyTorch binding of libminivllm_hip.so (kv_append, paged_decode, paged_prefill)";
+  m.doc() = "PyTorch binding of libminivllm_hip.so (kv_append, paged_decode, paged_decode_append, paged_prefill)";
   m.def("kv_append", &kv_append);
   m.def("paged_decode", &paged_decode);
+  m.def("paged_decode_append", &paged_decode_append);
   m.def("paged_prefill", &paged_prefill);
 }

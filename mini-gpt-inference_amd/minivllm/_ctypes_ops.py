@@ -1,4 +1,4 @@
-"""The eager path's three calls through ctypes, for when the _hip_ops
+"""The eager path's four calls through ctypes, for when the _hip_ops
 extension (csrc/torch_ops.cpp) cannot be loaded but libminivllm_hip.so can,
 for example after a PyTorch update that the extension was not rebuilt for.
 
@@ -62,9 +62,9 @@ def kv_append(kp: torch.Tensor, vp: torch.Tensor, layer_idx: int, k: torch.Tenso
         T, H, D, S, N, L, int(layer_idx), _native.stream_handle(kp.device)))
 
 
-def paged_decode(q: torch.Tensor, kp: torch.Tensor, vp: torch.Tensor, bt: torch.Tensor, cl: torch.Tensor,
-                 layer_idx: int, split_tokens: int) -> torch.Tensor:
-    """[B, H, D] decode attention output of q's dtype."""
+def _check_decode(q: torch.Tensor, kp: torch.Tensor, vp: torch.Tensor, bt: torch.Tensor, cl: torch.Tensor,
+                  layer_idx: int) -> int:
+    """paged_decode's checks; returns the block-table width M."""
     if not q.is_cuda:
         raise ValueError("q must be on a GPU device for the HIP backend")
     if q.ndim != 3:
@@ -99,6 +99,15 @@ def paged_decode(q: torch.Tensor, kp: torch.Tensor, vp: torch.Tensor, bt: torch.
     M = bt.shape[1]
     if M < 1:
         raise ValueError("block_tables need at least one block column")
+    return M
+
+
+def paged_decode(q: torch.Tensor, kp: torch.Tensor, vp: torch.Tensor, bt: torch.Tensor, cl: torch.Tensor,
+                 layer_idx: int, split_tokens: int) -> torch.Tensor:
+    """[B, H, D] decode attention output of q's dtype."""
+    M = _check_decode(q, kp, vp, bt, cl, layer_idx)
+    b, h, d = q.shape
+    L, N, S = kp.shape[:3]
     lib = _native.lib()
     out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
     ws_bytes = int(lib.mgi_paged_decode_workspace_bytes(b, h, d, S, M, int(split_tokens)))
@@ -106,6 +115,43 @@ def paged_decode(q: torch.Tensor, kp: torch.Tensor, vp: torch.Tensor, bt: torch.
     _native.check(lib.mgi_paged_decode(
         out.data_ptr(), _native.strides(out), q.data_ptr(), _native.strides(q),
         kp.data_ptr(), vp.data_ptr(), _native.strides(kp), _native.strides(vp), _native.DTYPE_CODES[q.dtype],
+        bt.data_ptr(), _native.strides(bt), _native.ITYPE_CODES[bt.dtype],
+        cl.data_ptr(), cl.stride(0), _native.ITYPE_CODES[cl.dtype],
+        b, h, d, S, N, M, L, int(layer_idx), 1.0 / math.sqrt(d), int(split_tokens),
+        ws.data_ptr() if ws is not None else None, ws_bytes, _native.stream_handle(q.device)))
+    return out
+
+
+def paged_decode_append(q: torch.Tensor, kp: torch.Tensor, vp: torch.Tensor, bt: torch.Tensor,
+                        cl: torch.Tensor, layer_idx: int, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor,
+                        split_tokens: int) -> torch.Tensor:
+    """kv_append of the B rows k[b], v[b] into slots[b], then paged_decode, as one call."""
+    M = _check_decode(q, kp, vp, bt, cl, layer_idx)
+    b, h, d = q.shape
+    L, N, S = kp.shape[:3]
+    if k.ndim != 3 or v.shape != k.shape:
+        raise ValueError("k and v must have matching shape [T,H,D]")
+    if k.shape[0] != b:
+        raise ValueError("k and v must hold one row per sequence")
+    if k.shape[1] != h or k.shape[2] != d:
+        raise ValueError("k/v head dimensions do not match the KV pool")
+    if k.dtype not in _FLOATS or v.dtype != k.dtype:
+        raise ValueError("k and v must share a float dtype")
+    if slots.ndim != 1 or slots.shape[0] != b:
+        raise ValueError("slot_mapping must have shape [B]")
+    if slots.dtype not in _INDEX:
+        raise ValueError("slot_mapping must contain integer slots")
+    if any(x.device != q.device for x in (k, v, slots)):
+        raise ValueError("all inputs must reside on same GPU device")
+    lib = _native.lib()
+    out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
+    ws_bytes = int(lib.mgi_paged_decode_workspace_bytes(b, h, d, S, M, int(split_tokens)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    _native.check(lib.mgi_paged_decode_append(
+        out.data_ptr(), _native.strides(out), q.data_ptr(), _native.strides(q),
+        kp.data_ptr(), vp.data_ptr(), _native.strides(kp), _native.strides(vp), _native.DTYPE_CODES[q.dtype],
+        k.data_ptr(), v.data_ptr(), _native.strides(k), _native.strides(v), _native.DTYPE_CODES[k.dtype],
+        slots.data_ptr(), slots.stride(0), _native.ITYPE_CODES[slots.dtype],
         bt.data_ptr(), _native.strides(bt), _native.ITYPE_CODES[bt.dtype],
         cl.data_ptr(), cl.stride(0), _native.ITYPE_CODES[cl.dtype],
         b, h, d, S, N, M, L, int(layer_idx), 1.0 / math.sqrt(d), int(split_tokens),

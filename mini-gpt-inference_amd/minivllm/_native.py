@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "mgi_abi_version",
     "mgi_kv_append",
     "mgi_paged_decode",
+    "mgi_paged_decode_append",
     "mgi_paged_decode_noalloc",
     "mgi_paged_decode_workspace_bytes",
     "mgi_paged_decode_split_tokens",
@@ -68,6 +69,20 @@ def _declare(lib: ctypes.CDLL) -> None:
         _p, _pi64,                         # out, strides
         _p, _pi64,                         # q, strides
         _p, _p, _pi64, _pi64, _i,          # pools, strides, dtype
+        _p, _pi64, _i,                     # block tables, strides, itype
+        _p, _i64, _i,                      # context lengths, stride, itype
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # B H D S N M L layer
+        ctypes.c_float, _i64,              # scale, split tokens
+        _p, ctypes.c_size_t,               # workspace, bytes
+        _p,                                # stream
+    ]
+    lib.mgi_paged_decode_append.restype = _i
+    lib.mgi_paged_decode_append.argtypes = [
+        _p, _pi64,                         # out, strides
+        _p, _pi64,                         # q, strides
+        _p, _p, _pi64, _pi64, _i,          # pools, strides, dtype
+        _p, _p, _pi64, _pi64, _i,          # new k/v, strides, dtype
+        _p, _i64, _i,                      # slot mapping, stride, itype
         _p, _pi64, _i,                     # block tables, strides, itype
         _p, _i64, _i,                      # context lengths, stride, itype
         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # B H D S N M L layer
@@ -121,8 +136,9 @@ def lib() -> ctypes.CDLL:
 
 
 def ops():
-    """The eager path's binding: kv_append, paged_decode and paged_prefill on
-    tensors, validated, calling the C ABI on the current stream.
+    """The eager path's binding: kv_append, paged_decode, paged_decode_append
+    and paged_prefill on tensors, validated, calling the C ABI on the current
+    stream.
 
     Normally the PyTorch extension _hip_ops (csrc/torch_ops.cpp). When the
     library loads but the extension does not (missing, or built against

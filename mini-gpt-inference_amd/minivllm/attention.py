@@ -6,10 +6,14 @@ decode attention -> output projection. The KV append completes before the
 attention reads the pool (same stream). The decode backend is chosen by name:
 
   "reference"          PyTorch: index_put_ KV write + paged_attention_batch_online_v1
-  "hip" / "triton_v0"  HIP kernels through libminivllm_hip.so: kv_append +
-                       paged_attention_batch_hip ("triton_v0" is accepted so
-                       callers that select the reference's Triton backend by
-                       name run the HIP kernels)
+  "hip" / "triton_v0"  HIP kernels through libminivllm_hip.so: the KV append
+                       and paged_attention_batch_hip as one call
+                       (paged_attention_batch_append_hip, which writes the
+                       new K/V inside the attention launch where it can), or
+                       as kv_append then paged_attention_batch_hip when
+                       ``fused_decode_append`` is False ("triton_v0" is
+                       accepted so callers that select the reference's Triton
+                       backend by name run the HIP kernels)
 
 With a HIP backend, prefill KV writes go through the same kv_append kernel
 (one launch per chunk instead of a per-token copy loop). Both HIP entry
@@ -95,6 +99,8 @@ class KVCacheCausalSelfAttention(nn.Module):
         self.prefill_prefix_fastpath_enabled = False
         self.prefill_hip = False
         self.decode_attention_backend = "reference"
+        # HIP backends: append and attend in one call (see the module docstring).
+        self.fused_decode_append = True
         self.qkv = nn.Linear(n_embd, 3 * n_embd, bias=False)
         self.register_buffer("tril", torch.tril(torch.ones(block_size, block_size)))
         self.attn_dropout = nn.Dropout(dropout)
@@ -231,13 +237,19 @@ class KVCacheCausalSelfAttention(nn.Module):
         elif backend in HIP_BACKENDS:
             if torch.is_grad_enabled() and q.requires_grad:
                 raise RuntimeError(f"{backend} is inference-only; run under torch.inference_mode()")
-            from .hip_paged_decode import kv_append, paged_attention_batch_hip
+            from . import hip_paged_decode as hpd
 
-            # The new token's K/V must be in the pool before attention reads it.
-            kv_append(kv_pool, layer_idx, k, v, metadata.slot_mapping)
-            out = paged_attention_batch_hip(q=q, pool=kv_pool, block_tables=metadata.block_tables,
-                                            context_lengths=metadata.context_lengths,
-                                            layer_idx=layer_idx)
+            if self.fused_decode_append:
+                # Row b's new K/V is sequence b's last token: the fused call's contract.
+                out = hpd.paged_attention_batch_append_hip(q, kv_pool, metadata.block_tables,
+                                                           metadata.context_lengths, layer_idx, k, v,
+                                                           metadata.slot_mapping)
+            else:
+                # The new token's K/V must be in the pool before attention reads it.
+                hpd.kv_append(kv_pool, layer_idx, k, v, metadata.slot_mapping)
+                out = hpd.paged_attention_batch_hip(q=q, pool=kv_pool, block_tables=metadata.block_tables,
+                                                    context_lengths=metadata.context_lengths,
+                                                    layer_idx=layer_idx)
         else:
             raise ValueError(f"unknown decode attention backend: {backend}")
         return self._finish(out.reshape(B, 1, C))

@@ -53,6 +53,26 @@ def paged_attention_batch_hip(q: torch.Tensor, pool: KVBlockPool, block_tables: 
                                       int(split_tokens))
 
 
+def paged_attention_batch_append_hip(q: torch.Tensor, pool: KVBlockPool, block_tables: torch.Tensor,
+                                     context_lengths: torch.Tensor, layer_idx: int, k: torch.Tensor,
+                                     v: torch.Tensor, slot_mapping: torch.Tensor, *,
+                                     split_tokens: int = 0) -> torch.Tensor:
+    """One decode step's KV write and attention as one call: kv_append of the
+    B rows k[b], v[b] ([B, H, D]) into slot_mapping[b], then
+    paged_attention_batch_hip, on the current stream.
+
+    Where the library can (bf16/f16/f32 rows of the pool's dtype, head dim
+    contiguous, 16-byte aligned, the fast attention path) the write runs inside
+    the attention launch, by the wavefront that streams each sequence's last
+    block, before it reads that block: one launch fewer per layer. The pool and
+    the output are bit-identical to the two calls, given the decode step's
+    invariant that a slot some context reads is the slot of its own row's last
+    position (``context_lengths[b] - 1``); negative slots are skipped.
+    """
+    return _native.ops().paged_decode_append(q, pool.k, pool.v, block_tables, context_lengths, int(layer_idx),
+                                             k, v, slot_mapping, int(split_tokens))
+
+
 def kv_append(pool: KVBlockPool, layer_idx: int, k: torch.Tensor, v: torch.Tensor,
               slot_mapping: torch.Tensor) -> None:
     """Scatters rows k[t], v[t] ([T, H, D], any strides) into pool slots slot_mapping[t].

@@ -1,12 +1,14 @@
 """Backend routing on the GPU, restating
 tests/test_decode_backend_integration.py:31-65 of the reference for the HIP
-backend: the attention entry point is patched (at
+backend: with the append and attention as two calls (fused_decode_append
+off), the attention entry point is patched (at
 minivllm.hip_paged_decode.paged_attention_batch_hip, where the model imports
 it at call time) with a stand-in that checks the new token's K/V are already
 in the pool -- written by the real kv_append kernel -- and then runs the
 PyTorch online-softmax attention. Logits and the written KV must then be
 bit-identical to the reference backend's (atol = rtol = 0): the append is a
-bitwise copy to the same slots, the reference writes with index_put_.
+bitwise copy to the same slots, the reference writes with index_put_. The
+default route, the fused call, must match the two calls bit for bit.
 """
 from __future__ import annotations
 
@@ -31,6 +33,8 @@ def test_route_appends_kv_before_attention_and_logits_identical(backend, dtype):
     torch.manual_seed(10)
     model = MiniGPT(n_embd=16, n_head=4, vocab_size=32, block_size=32, dropout=0.0, n_layer=2)
     model = model.eval().to(device=DEV, dtype=dtype)
+    for block in model.blocks:
+        block.attn.fused_decode_append = False
     inputs = torch.tensor([[1], [2]], dtype=torch.long, device=DEV)
     meta = DecodeBatchMetadata(positions=torch.tensor([0, 0], device=DEV),
                                context_lengths=torch.tensor([1, 1], device=DEV),
@@ -94,3 +98,45 @@ def test_unpatched_hip_route_matches_reference_within_tolerance():
     torch.testing.assert_close(got, ref, atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(p0.k[:, 1, 0], p1.k[:, 1, 0], atol=0, rtol=0)
     torch.testing.assert_close(p0.v[:, 0, 0], p1.v[:, 0, 0], atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_route_matches_two_calls_bit_for_bit(dtype):
+    """The default HIP route (the append inside the attention launch) against
+    the two calls, on a head dim the fused write takes (128): three decode
+    steps of 6 sequences over cached contexts, one of them padding; logits and
+    every pool byte identical at every step."""
+    torch.manual_seed(3)
+    model = MiniGPT(n_embd=256, n_head=2, vocab_size=64, block_size=512, dropout=0.0, n_layer=2)
+    model = model.eval().to(device=DEV, dtype=dtype)
+    model.set_decode_attention_backend("hip")
+    B, S, N, M = 6, 16, 128, 20
+    g = torch.Generator().manual_seed(4)
+    ctx0 = torch.randint(20, 300, (B,), generator=g)
+    perm = torch.randperm(N, generator=g)
+    tables = perm[:B * M].view(B, M).clone()
+    pools = []
+    for fused in (False, True):
+        pool = KVBlockPool(n_layer=2, num_blocks=N, block_size=S, n_head=2, head_dim=128, device=DEV, dtype=dtype)
+        gd = torch.Generator(device=DEV).manual_seed(5)
+        pool.k.normal_(generator=gd)
+        pool.v.normal_(generator=gd)
+        pools.append(pool)
+    for step in range(3):
+        pos = ctx0 + step
+        slots = tables[torch.arange(B), pos // S] * S + pos % S
+        slots[2] = -1   # a padding row: no write, attention over its cached context
+        ctx = torch.where(slots >= 0, pos + 1, pos)
+        meta = DecodeBatchMetadata(positions=pos.to(DEV), context_lengths=ctx.to(DEV),
+                                   block_tables=tables.to(DEV), slot_mapping=slots.to(DEV))
+        inputs = torch.randint(0, 64, (B, 1), generator=g).to(DEV)
+        outs = []
+        for fused, pool in zip((False, True), pools):
+            for block in model.blocks:
+                block.attn.fused_decode_append = fused
+            with torch.inference_mode():
+                outs.append(model.decode_batch(inputs, meta, pool))
+        torch.cuda.synchronize()
+        print(f"  fused route step {step} {dtype}", flush=True)
+        assert torch.equal(outs[0], outs[1])
+        assert torch.equal(pools[0].k, pools[1].k) and torch.equal(pools[0].v, pools[1].v)

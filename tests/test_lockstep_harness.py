@@ -38,6 +38,15 @@ def _cpu_attention(q, pool, block_tables, context_lengths, layer_idx, *, split_t
                                            context_lengths=context_lengths, layer_idx=layer_idx)
 
 
+def _fused(attention):
+    """A CPU stand-in for the fused append + attention call built from the two
+    stand-ins, in the two calls' order."""
+    def call(q, pool, block_tables, context_lengths, layer_idx, k, v, slot_mapping, *, split_tokens=0):
+        _cpu_kv_append(pool, layer_idx, k, v, slot_mapping)
+        return attention(q, pool, block_tables, context_lengths, layer_idx)
+    return call
+
+
 def _lockstep(**criterion) -> _e2e.Lockstep:
     model = _e2e.make_model(SPEC, torch.device("cpu"), torch.float32)
     return _e2e.Lockstep(SPEC, model, _e2e.make_prompts(SPEC), torch.device("cpu"), torch.float32,
@@ -72,6 +81,7 @@ def _run(ls: _e2e.Lockstep) -> None:
 
 @patch.object(hip_paged_decode, "paged_attention_batch_hip", _cpu_attention)
 @patch.object(hip_paged_decode, "kv_append", _cpu_kv_append)
+@patch.object(hip_paged_decode, "paged_attention_batch_append_hip", _fused(_cpu_attention))
 def test_forced_tie_keeps_every_row_in_the_checks():
     ls = _lockstep(logit_tol=(2e-5, 2e-4), tie_margin=1e9, kv_tol=(2e-5, 2e-4))
     planted = _plant_token(ls, at_call=3)
@@ -88,6 +98,7 @@ def test_forced_tie_keeps_every_row_in_the_checks():
 
 @patch.object(hip_paged_decode, "paged_attention_batch_hip", _cpu_attention)
 @patch.object(hip_paged_decode, "kv_append", _cpu_kv_append)
+@patch.object(hip_paged_decode, "paged_attention_batch_append_hip", _fused(_cpu_attention))
 def test_token_difference_outside_a_tie_fails():
     ls = _lockstep(logit_tol=(2e-5, 2e-4), tie_margin=0.0, kv_tol=(2e-5, 2e-4))
     _plant_token(ls, at_call=2)
@@ -102,6 +113,7 @@ def _shifted_attention(q, pool, block_tables, context_lengths, layer_idx, *, spl
 
 @patch.object(hip_paged_decode, "paged_attention_batch_hip", _shifted_attention)
 @patch.object(hip_paged_decode, "kv_append", _cpu_kv_append)
+@patch.object(hip_paged_decode, "paged_attention_batch_append_hip", _fused(_shifted_attention))
 def test_attention_error_past_the_bound_fails():
     ls = _lockstep(logit_tol=(2e-5, 2e-4), tie_margin=1e9, kv_tol=(2e-5, 2e-4))
     with pytest.raises(AssertionError, match="decode logits differ"):

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.lib()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.mgi_abi_version() == 103
+    assert lib.mgi_abi_version() == 104
 
 
 def test_torch_binding_loads_and_validates_on_the_host():
@@ -37,7 +37,7 @@ def test_torch_binding_loads_and_validates_on_the_host():
     and raises the wrappers' ValueErrors before any device work: CPU tensors
     are refused first."""
     ops = _native.ops()
-    for name in ("kv_append", "paged_decode", "paged_prefill"):
+    for name in ("kv_append", "paged_decode", "paged_decode_append", "paged_prefill"):
         assert callable(getattr(ops, name)), name
     from minivllm import hip_paged_decode as hpd
     from minivllm.kv_block_pool import KVBlockPool
@@ -51,6 +51,10 @@ def test_torch_binding_loads_and_validates_on_the_host():
         hpd.kv_append(pool, 0, q, q, torch.zeros(1, dtype=torch.long))
     with pytest.raises(ValueError, match="q must be on a GPU device"):
         hpd.paged_prefill_hip(q, pool, torch.zeros(1, dtype=torch.long), 0, 0)
+    with pytest.raises(ValueError, match="q must be on a GPU device"):
+        hpd.paged_attention_batch_append_hip(q, pool, torch.zeros(1, 1, dtype=torch.long),
+                                             torch.ones(1, dtype=torch.long), 0, q, q,
+                                             torch.zeros(1, dtype=torch.long))
 
 
 def test_ctypes_path_when_the_extension_cannot_load(monkeypatch, tmp_path):
@@ -75,6 +79,10 @@ def test_ctypes_path_when_the_extension_cannot_load(monkeypatch, tmp_path):
         hpd.kv_append(pool, 0, q, q, torch.zeros(1, dtype=torch.long))
     with pytest.raises(ValueError, match="^q must be on a GPU device for the HIP backend$"):
         hpd.paged_prefill_hip(q, pool, torch.zeros(1, dtype=torch.long), 0, 0)
+    with pytest.raises(ValueError, match="^q must be on a GPU device for the HIP backend$"):
+        hpd.paged_attention_batch_append_hip(q, pool, torch.zeros(1, 1, dtype=torch.long),
+                                             torch.ones(1, dtype=torch.long), 0, q, q,
+                                             torch.zeros(1, dtype=torch.long))
 
 
 def test_missing_library_is_an_error_not_a_fallback(monkeypatch, tmp_path):
@@ -166,6 +174,39 @@ def test_paged_decode_rejects_bad_arguments_on_host():
     ]
     for kw, msg in cases:
         assert call(**kw) == _native.MGI_EINVAL or call(**kw) == _native.MGI_EUNSUPPORTED, kw
+        assert msg in lib.mgi_last_error().decode(), (kw, lib.mgi_last_error())
+
+
+def test_paged_decode_append_rejects_bad_arguments_on_host():
+    """The fused append + decode entry checks both calls' arguments before any
+    launch (the pointers are never dereferenced)."""
+    lib = _native.lib()
+    st3, st5, st2 = _i64(1, 1, 1), _i64(1, 1, 1, 1, 1), _i64(1, 1)
+    fake = 0x1000
+
+    def call(**kw):
+        a = dict(out=fake, q=fake, k=fake, v=fake, dtype=_native.MGI_BF16, kn=fake, vn=fake,
+                 new_dtype=_native.MGI_BF16, slots=fake, sl_it=1, sl_s=1, bt=fake, cl=fake, B=1, H=1, D=8,
+                 S=16, N=4, M=1, L=1, layer=0)
+        a.update(kw)
+        return lib.mgi_paged_decode_append(
+            a["out"], st3, a["q"], st3, a["k"], a["v"], st5, st5, a["dtype"], a["kn"], a["vn"], st3, st3,
+            a["new_dtype"], a["slots"], a["sl_s"], a["sl_it"], a["bt"], st2, 1, a["cl"], 1, 1, a["B"], a["H"],
+            a["D"], a["S"], a["N"], a["M"], a["L"], a["layer"], 0.5, 0, None, 0, None)
+
+    cases = [
+        (dict(q=None), "null tensor pointer"),
+        (dict(kn=None), "null tensor pointer"),
+        (dict(slots=None), "null tensor pointer"),
+        (dict(B=0), "q dimensions must be nonzero"),
+        (dict(layer=1), "layer_idx outside KV pool"),
+        (dict(sl_it=4), "slot_mapping must be int32 or int64"),
+        (dict(sl_s=-1), "strides must be non-negative"),
+        (dict(new_dtype=5), "unknown dtype"),
+        (dict(new_dtype=_native.MGI_F16), "only same-dtype copies and conversions to/from f32"),
+    ]
+    for kw, msg in cases:
+        assert call(**kw) in (_native.MGI_EINVAL, _native.MGI_EUNSUPPORTED), kw
         assert msg in lib.mgi_last_error().decode(), (kw, lib.mgi_last_error())
 
 

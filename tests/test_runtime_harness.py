@@ -287,7 +287,11 @@ def test_default_backend_and_validation():
 
 
 def test_hip_route_writes_kv_before_attention_and_matches_reference_bitwise():
+    """The reference's routing test (two calls: the KV write, then the backend)
+    on the HIP route with fused_decode_append off."""
     model = _model()
+    for block in model.blocks:
+        block.attn.fused_decode_append = False
     inputs = torch.tensor([[1], [2]], dtype=torch.long)
     meta = DecodeBatchMetadata(positions=torch.tensor([0, 0]), context_lengths=torch.tensor([1, 1]),
                                block_tables=torch.tensor([[1], [0]], dtype=torch.long),
@@ -324,6 +328,41 @@ def test_hip_route_writes_kv_before_attention_and_matches_reference_bitwise():
     torch.testing.assert_close(expected, actual, atol=0, rtol=0)
     torch.testing.assert_close(pool0.k[:, 1, 0], pool1.k[:, 1, 0], atol=0, rtol=0)
     torch.testing.assert_close(pool0.v[:, 0, 0], pool1.v[:, 0, 0], atol=0, rtol=0)
+
+
+def test_fused_hip_route_passes_the_step_rows_and_matches_reference_bitwise():
+    """The default HIP route makes one call per layer with the step's q, k, v
+    and slot mapping (a stand-in does the write and the reference attention):
+    logits and KV bit-identical to the reference backend."""
+    model = _model()
+    inputs = torch.tensor([[1], [2]], dtype=torch.long)
+    meta = DecodeBatchMetadata(positions=torch.tensor([0, 0]), context_lengths=torch.tensor([1, 1]),
+                               block_tables=torch.tensor([[1], [0]], dtype=torch.long),
+                               slot_mapping=torch.tensor([16, 0], dtype=torch.long))
+    pools = []
+    for _ in range(2):
+        pool = KVBlockPool(n_layer=2, num_blocks=2, block_size=16, n_head=4, head_dim=4)
+        pool.k.fill_(float("nan"))
+        pool.v.fill_(float("nan"))
+        pools.append(pool)
+    calls = []
+
+    def fake_fused(q, pool, block_tables, context_lengths, layer_idx, k, v, slot_mapping):
+        calls.append(layer_idx)
+        assert q.shape == k.shape == v.shape == (2, 4, 4) and slot_mapping is meta.slot_mapping
+        pool.k[layer_idx, slot_mapping // 16, slot_mapping % 16] = k
+        pool.v[layer_idx, slot_mapping // 16, slot_mapping % 16] = v
+        return paged_attention_batch_online_v1(q, pool, block_tables, context_lengths, layer_idx)
+
+    with torch.inference_mode():
+        model.set_decode_attention_backend("reference")
+        expected = model.decode_batch(inputs, meta, pools[0])
+        model.set_decode_attention_backend("hip")
+        with patch("minivllm.hip_paged_decode.paged_attention_batch_append_hip", side_effect=fake_fused):
+            actual = model.decode_batch(inputs, meta, pools[1])
+    assert calls == [0, 1]
+    torch.testing.assert_close(expected, actual, atol=0, rtol=0)
+    torch.testing.assert_close(pools[0].k[:, 1, 0], pools[1].k[:, 1, 0], atol=0, rtol=0)
 
 
 @pytest.mark.parametrize("backend", ["hip", "triton_v0"])
