@@ -225,7 +225,10 @@ def c3_step_line(steps, warmup, dev):
     token is appended at slot table[ctx // 16] * 16 + ctx % 16 (a fresh block
     when ctx % 16 == 0), 10 % of the rows are padding (slot -1), then decode
     attention runs over ctx + 1 tokens for appended rows and ctx for padded
-    ones. The append and the attention are timed together, on one pool."""
+    ones. The append and the attention are timed together, on one pool: as
+    the two calls (kv_append, then paged decode) and as the one fused call
+    (paged_attention_batch_append_hip, the runtime's default), whose outputs
+    are checked bit-identical to the two calls'."""
     import torch
 
     import _fixtures as fx
@@ -259,16 +262,24 @@ def c3_step_line(steps, warmup, dev):
 
     def step():
         hpd.kv_append(pool, 0, k_new, v_new, slots_d)
-        hpd.paged_attention_batch_hip(q, pool, tables_d, lens_d, 0)
+        return hpd.paged_attention_batch_hip(q, pool, tables_d, lens_d, 0)
 
+    def fused():
+        return hpd.paged_attention_batch_append_hip(q, pool, tables_d, lens_d, 0, k_new, v_new, slots_d)
+
+    same = bool(torch.equal(step(), fused()))
     ms = time_calls(step, steps, warmup)["median_ms"]
+    ms_fused = time_calls(fused, steps, warmup)["median_ms"]
     n_valid = int((~pad).sum())
     append_bytes = n_valid * H * D * 2 * 2 * 2 + B * 8
     attn_bytes = fx.DecodeWorkload(q, pool, tables_d, lens_d, 0, {}).algorithmic_bytes()
     gbps = (append_bytes + attn_bytes) / (ms * 1e-3) / 1e9
+    gbps_fused = (append_bytes + attn_bytes) / (ms_fused * 1e-3) / 1e9
     return {"us": round(ms * 1e3, 2), "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+            "fused_us": round(ms_fused * 1e3, 2), "fused_pct_of_peak": round(100 * gbps_fused / PEAK_GBPS, 2),
+            "fused_bit_identical": same,
             "append_bytes": append_bytes, "attention_bytes": attn_bytes, "valid_rows": n_valid,
-            "sum_ctx": int(lens.sum()), "rows_per_s_per_layer": round(B / (ms * 1e-3), 1)}
+            "sum_ctx": int(lens.sum()), "rows_per_s_per_layer": round(B / (ms_fused * 1e-3), 1)}
 
 
 def copy_line(mib: int, dev, reps: int = 3):
