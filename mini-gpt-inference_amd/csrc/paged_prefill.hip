@@ -629,16 +629,18 @@ __device__ __align__(16) const unsigned char kZeroRow[512] = {0};
 template <typename T> struct TrRead;
 template <> struct TrRead<bf16_t> {
   typedef __bf16 v4 __attribute__((ext_vector_type(4)));
-  __device__ static __forceinline__ uint2 read(const unsigned char* p) {
+  // From an LDS byte address: constant terms added to it fold into the
+  // instruction's offset field.
+  __device__ static __forceinline__ uint2 at(uint32_t addr) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                                         (__attribute__((address_space(3))) v4*)(p)));
+                                         (__attribute__((address_space(3))) v4*)(uintptr_t)addr));
   }
 };
 template <> struct TrRead<f16_t> {
   typedef __fp16 v4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
-  __device__ static __forceinline__ uint2 read(const unsigned char* p) {
+  __device__ static __forceinline__ uint2 at(uint32_t addr) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                                         (__attribute__((address_space(3))) v4*)(p)));
+                                         (__attribute__((address_space(3))) v4*)(uintptr_t)addr));
   }
 };
 
@@ -906,10 +908,12 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       cp.kb[j] = kbase + (uint64_t)phys * k_sn2 + inb * k_ss2;
       cp.vb[j] = vbase + (uint64_t)phys * v_sn2 + inb * v_ss2;
     }
-    vm = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (cp.live && ((valid >> j) & 1u)) vm |= 0xffffull << (16 * j);
+    // Bit j of `valid` spread to bits 16j .. 16j + 15 (two 32-bit halves,
+    // each a product with 0xffff of bits 16 apart).
+    const uint32_t vl = cp.live ? valid : 0u;
+    const uint32_t lo = ((vl & 1u) | ((vl & 2u) << 15)) * 0xffffu;
+    const uint32_t hi = (((vl >> 2) & 1u) | ((vl & 8u) << 13)) * 0xffffu;
+    vm = ((uint64_t)hi << 32) | lo;
     return cp;
   };
   // Issues copy i (one K and one V row group) of a plan. The LDS
@@ -918,14 +922,13 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   // sum out of the loop: held in scalar registers, those sums (one per
   // copy, stage and group) ran past the register file and were spilled to
   // vector-register lanes, a v_readlane per copy.
-  auto copy_one = [&](const CopyPlan& cp, int i) __attribute__((always_inline)) {
-    if (!cp.live) return;
+  auto copy_one = [&](const CopyPlan& cp, int i, auto fast) __attribute__((always_inline)) {
     const int j = i / CPGW;
     uint32_t kd = k_dst0, vd = v_dst0;
     asm volatile("" : "+s"(kd), "+s"(vd));
     kd += cp.kdst + i * 1024;
     vd += cp.vdst + i * 1024;
-    if (cp.fast) {
+    if constexpr (decltype(fast)::value) {
       copy16_to_lds(cp.kb[j], koff[i], kd);
       copy16_to_lds(cp.vb[j], voff[i], vd);
     } else {
@@ -937,9 +940,16 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
       copy16_to_lds(vs, vd);
     }
   };
+  // One branch per tile: the full-tile form's copies, or the masked form's.
   auto copy_all = [&](const CopyPlan& cp) __attribute__((always_inline)) {
+    if (!cp.live) return;
+    if (cp.fast) {
 #pragma unroll
-    for (int i = 0; i < GPW; ++i) copy_one(cp, i);
+      for (int i = 0; i < GPW; ++i) copy_one(cp, i, Stage<1>{});
+    } else {
+#pragma unroll
+      for (int i = 0; i < GPW; ++i) copy_one(cp, i, Stage<0>{});
+    }
   };
 
   // Running sums of P come out of the PV products: lacc[b] = ones^T P^T, a
@@ -975,10 +985,11 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   for (int f = 0; f < NQF; ++f) ka[f] = kbuf0 * TILEB + krb * ROWB + (((4 * f + g) ^ k_swz<CPR>(krb)) << 4);
   const int tr_j = (lane & 15) >> 2, tr_q = lane & 3;
   const int vr = 8 * g + tr_j;
-  int va[NDB];
+  uint32_t va[NDB];  // LDS byte addresses
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
-    va[db] = vbuf0 * TILEB + vr * ROWB + ((tr_q & 1) << 3) + (((2 * db + (tr_q >> 1)) ^ v_swz<CPR>(vr)) << 4);
+    va[db] = lds_addr(v_lds) + vbuf0 * TILEB + vr * ROWB + ((tr_q & 1) << 3) +
+             (((2 * db + (tr_q >> 1)) ^ v_swz<CPR>(vr)) << 4);
   const float cs = query_scale(a.scale_log2);  // the query carries the sign (query_sign)
   const float inv_cs = 1.f / cs;
 
@@ -1070,14 +1081,13 @@ __global__ __launch_bounds__(64 * WAVES * GROUPS) void paged_prefill_tr(const Pr
   // slice c; each V read feeds QPW products.
   auto pv = [&](auto bm, int ST, const uint4 (&pb)[QPW][2]) __attribute__((always_inline)) {
     constexpr int BM = decltype(bm)::value;
-    const unsigned char* vl = v_lds + ST * TILEB;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       uint4 vv[NDB];
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const uint2 lo = TrRead<T>::read(vl + va[db] + (32 * c) * ROWB);
-        const uint2 hi = TrRead<T>::read(vl + va[db] + (32 * c + 4) * ROWB);
+        const uint2 lo = TrRead<T>::at(va[db] + ST * TILEB + (32 * c) * ROWB);
+        const uint2 hi = TrRead<T>::at(va[db] + ST * TILEB + (32 * c + 4) * ROWB);
         vv[db] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
 #pragma unroll
