@@ -167,6 +167,19 @@ def test_shapes_taking_the_separate_append_kernel(variant):
         assert_identical(*run_both(c, k=kt, v=vt))
 
 
+@pytest.mark.parametrize("dtype,split", [(torch.bfloat16, 0), (torch.float32, 0), (torch.bfloat16, 64)],
+                         ids=["bf16_even", "f32_even", "bf16_partitions"])
+def test_int32_tables_lengths_and_slots(dtype, split):
+    """int32 block tables, context lengths and slot mapping (the fused write
+    reads the slot of a tail row and of a row with no blocks through the
+    same index loads as the attention)."""
+    c = step_case(21, 8, 128, 16, 1, 400, dtype, seed=17)
+    for key in ("tables", "ctx", "slots"):
+        c[key] = c[key].to(torch.int32)
+    assert "empty" in c["kinds"] and "pad" in c["kinds"]
+    assert_identical(*run_both(c, split_tokens=split))
+
+
 def test_rows_from_a_fused_qkv_view():
     """The model's layout: k and v are views of one [B, 3, H, D] projection
     (row stride 3 H D), q a third view."""
