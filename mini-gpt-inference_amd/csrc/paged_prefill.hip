@@ -1336,15 +1336,20 @@ int prefill_tr_mode() {
 //     14.5), and first chunks (start 0) whose 64-row tiles take up to two
 //     rounds of the CUs (1536 rows: 26.8 against 31.3 for 412; 8 heads,
 //     3072 rows: 40.5 against 54.1);
-//   * 412 (two workgroups of four 16-row wavefronts per CU) otherwise, and
-//     whenever the keys are split over workgroups (its cost model assumes
-//     64-row tiles).
+//   * with the keys split over workgroups (the cost model sizes partitions
+//     for 64-row tiles): 1422 when its 128-row tiles times the partitions
+//     fill the CUs and a partition holds at least 16 key tiles (512 rows
+//     after 16 384: 83 against 98 us for 412; after 8192: 51 / 58; 256 rows
+//     after 8192: 36 / 37), else 412 (256 after 4096: 27 against 29 for
+//     1422, whose two-group hand-over does not pay on 9-tile partitions);
+//   * 412 (two workgroups of four 16-row wavefronts per CU) otherwise.
 int prefill_tr_choice(const PrefillArgs& a) {
   const int forced = prefill_tr_mode();
   if (forced >= 0) return forced;
   const int64_t wgs128 = ((int64_t)a.T + 127) / 128 * a.H, wgs64 = ((int64_t)a.T + 63) / 64 * a.H;
   const int64_t wgs_paired = (((int64_t)a.T + 63) / 64 + 1) / 2 * a.H;
-  if (a.part_keys > 0) return 412;
+  if (a.part_keys > 0)
+    return wgs128 * a.max_parts >= a.cus && a.part_keys >= 16 * kTileKeys ? 1422 : 412;
   if (wgs_paired <= a.cus && 8 * wgs_paired >= 7 * (int64_t)a.cus) return 11422;
   const int64_t mean_keys = (int64_t)a.start + a.T / 2;  // keys the mean query tile attends to
   if (wgs128 >= a.cus && (a.start >= a.T || (wgs128 > a.cus && mean_keys >= 20 * kTileKeys))) return 1422;
