@@ -1342,7 +1342,9 @@ int prefill_tr_mode() {
 //     after 16 384: 83 against 98 us for 412; after 8192: 51 / 58; 256 rows
 //     after 8192: 36 / 37), else 412 (256 after 4096: 27 against 29 for
 //     1422, whose two-group hand-over does not pay on 9-tile partitions);
-//   * 412 (two workgroups of four 16-row wavefronts per CU) otherwise.
+//   * 412 (two workgroups of four 16-row wavefronts per CU) otherwise, and
+//     for chunks whose keys fit one tile (64 rows at 0, 16 and 32 heads:
+//     8.4-8.5 against 9.4-9.6 us for 1412).
 int prefill_tr_choice(const PrefillArgs& a) {
   const int forced = prefill_tr_mode();
   if (forced >= 0) return forced;
@@ -1350,6 +1352,7 @@ int prefill_tr_choice(const PrefillArgs& a) {
   const int64_t wgs_paired = (((int64_t)a.T + 63) / 64 + 1) / 2 * a.H;
   if (a.part_keys > 0)
     return wgs128 * a.max_parts >= a.cus && a.part_keys >= 16 * kTileKeys ? 1422 : 412;
+  if (a.start + a.T <= kTileKeys) return 412;  // one key tile: a second group would idle
   if (wgs_paired <= a.cus && 8 * wgs_paired >= 7 * (int64_t)a.cus) return 11422;
   const int64_t mean_keys = (int64_t)a.start + a.T / 2;  // keys the mean query tile attends to
   if (wgs128 >= a.cus && (a.start >= a.T || (wgs128 > a.cus && mean_keys >= 20 * kTileKeys))) return 1422;
