@@ -1338,10 +1338,11 @@ int prefill_tr_mode() {
 //     3072 rows: 40.5 against 54.1);
 //   * with the keys split over workgroups (the cost model sizes partitions
 //     for 64-row tiles): 1422 when its 128-row tiles times the partitions
-//     fill the CUs and a partition holds at least 16 key tiles (512 rows
-//     after 16 384: 83 against 98 us for 412; after 8192: 51 / 58; 256 rows
-//     after 8192: 36 / 37), else 412 (256 after 4096: 27 against 29 for
-//     1422, whose two-group hand-over does not pay on 9-tile partitions);
+//     fill the CUs and a partition holds at least 32 key tiles (512 rows
+//     after 16 384: 83 against 98 us for 412; after 8192: 51.7 / 58.4; 32
+//     heads, 256 after 8192: 53 / 58), else 412 (256 after 4096: 27 against
+//     29 for 1422; 32 heads, 512 after 2048, 19-tile partitions: 45.6 /
+//     48.6), whose two-group hand-over does not pay on short partitions;
 //   * 412 (two workgroups of four 16-row wavefronts per CU) otherwise, and
 //     for chunks whose keys fit one tile (64 rows at 0, 16 and 32 heads:
 //     8.4-8.5 against 9.4-9.6 us for 1412).
@@ -1351,7 +1352,7 @@ int prefill_tr_choice(const PrefillArgs& a) {
   const int64_t wgs128 = ((int64_t)a.T + 127) / 128 * a.H, wgs64 = ((int64_t)a.T + 63) / 64 * a.H;
   const int64_t wgs_paired = (((int64_t)a.T + 63) / 64 + 1) / 2 * a.H;
   if (a.part_keys > 0)
-    return wgs128 * a.max_parts >= a.cus && a.part_keys >= 16 * kTileKeys ? 1422 : 412;
+    return wgs128 * a.max_parts >= a.cus && a.part_keys >= 32 * kTileKeys ? 1422 : 412;
   if (a.start + a.T <= kTileKeys) return 412;  // one key tile: a second group would idle
   if (wgs_paired <= a.cus && 8 * wgs_paired >= 7 * (int64_t)a.cus) return 11422;
   const int64_t mean_keys = (int64_t)a.start + a.T / 2;  // keys the mean query tile attends to

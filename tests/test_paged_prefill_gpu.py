@@ -242,13 +242,13 @@ def test_prefill_kernel_configs_f16_masked_and_split(monkeypatch, config, split_
     assert torch.count_nonzero(out0[:16]) == 0
 
 
-@pytest.mark.parametrize("start,T,H", [(3000, 256, 8), (8192, 256, 16)], ids=["412_split", "1422_split"])
+@pytest.mark.parametrize("start,T,H", [(3000, 256, 8), (8192, 256, 32)], ids=["412_split", "1422_split"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_key_split_agrees_with_unsplit(monkeypatch, dtype, start, T, H):
     """The automatic split (a small chunk after a long prefix) against the
     same call with the split turned off: same softmax, summed in another
-    order. After 8192 keys the partitions hold 17 key tiles and the split
-    runs on 128-row workgroups; after 3000, on 64-row ones."""
+    order. After 8192 keys with 32 heads the partitions hold 33 key tiles
+    and the split runs on 128-row workgroups; after 3000, on 64-row ones."""
     D, S = 128, 16
     lib = hpd._native.lib()
     assert lib.mgi_paged_prefill_workspace_bytes(start, T, H, D, hpd._native.DTYPE_CODES[dtype]) > 0
