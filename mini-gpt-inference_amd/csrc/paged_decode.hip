@@ -526,16 +526,23 @@ __device__ __forceinline__ size_t bal_slot(const DecodeArgs& a, const Claims& c,
   return ((size_t)h * a.bal_claims + i) * 2 + (claim_begin(c, i) >= cb ? 0 : 1);
 }
 
-// Inclusive prefix sums of ceil(ctx_b / S) into cinc[0 .. B); returns the
-// total (uniform). One wavefront: lane i covers sequences [i*K, i*K + K).
+// Inclusive prefix sums of ceil(ctx_b / S) into cinc[0 .. B) and the
+// clamped context lengths into cctx[0 .. B) (a wave entering a sequence then
+// reads its length from LDS instead of waiting on a global load before its
+// table loads); returns the total (uniform). One wavefront: lane i covers
+// sequences [i*K, i*K + K).
 template <typename T>
-__device__ __forceinline__ int seq_block_scan(const DecodeArgs& a, int lane, int* cinc) {
+__device__ __forceinline__ int seq_block_scan(const DecodeArgs& a, int lane, int* cinc, int* cctx) {
   const int K = (a.B + 63) / 64;
   const int b0 = lane * K;
   int sum = 0;
   for (int k = 0; k < K; ++k) {
     const int b = b0 + k;
-    if (b < a.B) sum += (clamp_ctx<T>(a, b) + a.S - 1) / a.S;
+    if (b < a.B) {
+      const int c = clamp_ctx<T>(a, b);
+      cctx[b] = c;
+      sum += (c + a.S - 1) / a.S;
+    }
   }
   int incl = sum;
 #pragma unroll
@@ -547,7 +554,7 @@ __device__ __forceinline__ int seq_block_scan(const DecodeArgs& a, int lane, int
   for (int k = 0; k < K; ++k) {
     const int b = b0 + k;
     if (b < a.B) {
-      run += (clamp_ctx<T>(a, b) + a.S - 1) / a.S;
+      run += (cctx[b] + a.S - 1) / a.S;
       cinc[b] = run;
     }
   }
@@ -565,7 +572,7 @@ template <typename T, int LPH, int TOK, bool FULL>
 __global__ void __launch_bounds__(64)
 paged_decode_fast_bal(const DecodeArgs a) {
   constexpr int HPW = 64 / LPH;
-  __shared__ int cinc[kBalMaxB];
+  __shared__ int cinc[kBalMaxB], cctx[kBalMaxB];
   const int lane = (int)threadIdx.x;
   const int sub = lane % LPH;
   const int ngroups = (a.H + HPW - 1) / HPW;
@@ -589,7 +596,7 @@ paged_decode_fast_bal(const DecodeArgs a) {
   const int h = hg * HPW + lane / LPH;
   const bool lane_ok = FULL || (h < a.H && sub * 8 < a.D);
 
-  const int total = seq_block_scan<T>(a, lane, cinc);
+  const int total = seq_block_scan<T>(a, lane, cinc, cctx);
   if (blockIdx.x == 0)  // the merge reads the block list from the workspace
     for (int i = lane; i < a.B; i += 64) a.ws_cinc[i] = cinc[i];
   const Claims cl = make_claims(a, total);
@@ -646,7 +653,7 @@ paged_decode_fast_bal(const DecodeArgs a) {
       if (pos >= ce) {  // entering sequence b
         cb = b > 0 ? uread(cinc, b - 1) : 0;
         ce = uread(cinc, b);
-        ctx = clamp_ctx<T>(a, b);
+        ctx = uread(cctx, b);
         load_query<T>(a, b, h, sub, lane_ok, q);
         m = -INFINITY;
         l = 0.f;
